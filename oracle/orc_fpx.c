@@ -1,0 +1,177 @@
+/* orc_fpx.c -- fp32 <-> fixed-point limb planes (src/fpfixed.c).
+ * Test infrastructure only (see oracle.h).
+ *
+ * Every finite nonzero fp32 x is mi * 2^e2 with mi in [2^23, 2^24).  On a
+ * grid of scale 2^S the integer x * 2^S is mi shifted left by e2 + S; that
+ * shifted significand is written straight into (at most) three signed
+ * base-2^16 limbs.  The exact product comes back at scale 2^(SA+SB) and is
+ * rounded once, to nearest-even, to 24 significant bits. */
+#include <stdlib.h>
+#include <string.h>
+#include <math.h>
+#include "oracle.h"
+
+static int next_pow2(int x) { int r = 1; while (r < x) r <<= 1; return r; }
+
+/* src/fpfixed.c:40-54 */
+static void exp_range(const float *X, size_t cnt, int *lo, int *hi, int *any)
+{
+    int l = 1 << 30, h = -(1 << 30), seen = 0;
+    for (size_t i = 0; i < cnt; i++) {
+        float x = X[i];
+        if (x == 0.0f || !isfinite(x)) continue;
+        int e;
+        frexpf(x, &e);
+        if (e - 24 < l) l = e - 24;
+        if (e - 24 > h) h = e - 24;
+        seen = 1;
+    }
+    if (!seen) { l = 0; h = 0; }
+    *lo = l; *hi = h; *any = seen;
+}
+
+/* src/fpfixed.c:59-108 (fp32: 24-bit significand, touches <= 3 limbs). */
+int orc_fpx_init(orc_fpx *c, const float *A, const float *B, int n,
+                 int force_bits)
+{
+    size_t nn = (size_t)n * n;
+    int loA, hiA, loB, hiB, anyA, anyB;
+    exp_range(A, nn, &loA, &hiA, &anyA);
+    exp_range(B, nn, &loB, &hiB, &anyB);
+    memset(c, 0, sizeof *c);
+    c->spreadA = anyA ? hiA - loA : 0;
+    c->spreadB = anyB ? hiB - loB : 0;
+    int L;
+    if (force_bits > 0) {
+        c->SA = c->SB = force_bits / 2;
+        L = next_pow2(force_bits / ORC_LIMB_BITS);
+    } else {
+        c->SA = -loA;
+        c->SB = -loB;
+        int bits = 24 + (c->spreadA > c->spreadB ? c->spreadA : c->spreadB) + 1;
+        int spread = c->spreadA > c->spreadB ? c->spreadA : c->spreadB;
+        int need = (bits + ORC_LIMB_BITS - 1) / ORC_LIMB_BITS;
+        int need2 = spread / ORC_LIMB_BITS + 3;
+        L = next_pow2(need > need2 ? need : need2);
+        if (L < 2) L = 2;
+    }
+    c->n = n; c->L = L;
+    /* src/fpfixed.c:84-88: refuse sizes whose int64 accumulators could
+     * overflow. */
+    if ((double)n * L * 65535.0 * 65535.0 > 4.0e18) return -1;
+    c->A32 = calloc((size_t)L * nn, sizeof(int32_t));
+    c->B32 = calloc((size_t)L * nn, sizeof(int32_t));
+    c->Cw = calloc((size_t)(2 * L - 1) * nn, sizeof(int64_t));
+    if (!c->A32 || !c->B32 || !c->Cw) { orc_fpx_free(c); return -1; }
+    return 0;
+}
+
+/* src/fpfixed.c:175-193: zero, Inf and NaN are skipped; an offset below the
+ * grid drops the value; limbs at or above L are dropped. */
+static void encode_one(int32_t *planes, size_t nn, size_t idx, float x,
+                       int L, int S)
+{
+    if (x == 0.0f || !isfinite(x)) return;
+    int e;
+    float m = frexpf(x, &e);
+    int32_t mi = (int32_t)(fabsf(m) * 16777216.0f);
+    int off = e - 24 + S;
+    if (off < 0) return;
+    int lo = off >> 4, sh = off & 15;
+    uint64_t v = (uint64_t)mi << sh;
+    int sgn = x < 0.0f ? -1 : 1;
+    for (int t = 0; t < 3 && lo + t < L; t++)
+        planes[(size_t)(lo + t) * nn + idx] = sgn * (int32_t)((v >> (16 * t)) & 0xFFFFu);
+}
+
+void orc_fpx_encode(orc_fpx *c, const float *A, const float *B)
+{
+    size_t nn = (size_t)c->n * c->n;
+    memset(c->A32, 0, sizeof(int32_t) * (size_t)c->L * nn);
+    memset(c->B32, 0, sizeof(int32_t) * (size_t)c->L * nn);
+    for (size_t i = 0; i < nn; i++) encode_one(c->A32, nn, i, A[i], c->L, c->SA);
+    for (size_t i = 0; i < nn; i++) encode_one(c->B32, nn, i, B[i], c->L, c->SB);
+}
+
+/* src/fpfixed.c:212-251: carry over 2L+2 limbs with an arithmetic shift;
+ * a negative result is negated in two's complement; then the top <= 4
+ * nonzero limbs and a sticky bit for everything below. Returns the sign
+ * (0 for an exact zero). */
+static int extract(const int64_t *Cw, int L, size_t nn, size_t idx,
+                   int32_t *limb, uint64_t *top, int *tb, int *shift,
+                   int *sticky)
+{
+    int RL = 2 * L + 2, P = 2 * L - 1;
+    int64_t carry = 0;
+    for (int w = 0; w < RL; w++) {
+        int64_t t = carry + (w < P ? Cw[(size_t)w * nn + idx] : 0);
+        limb[w] = (int32_t)(t & 0xFFFF);
+        carry = t >> ORC_LIMB_BITS;
+    }
+    int neg = carry < 0;
+    if (neg) {
+        int32_t borrow = 1;
+        for (int w = 0; w < RL; w++) {
+            int32_t t = (~limb[w] & 0xFFFF) + borrow;
+            limb[w] = t & 0xFFFF;
+            borrow = t >> ORC_LIMB_BITS;
+        }
+    }
+    int h = -1;
+    for (int w = RL - 1; w >= 0; w--) if (limb[w]) { h = w; break; }
+    if (h < 0) return 0;
+    int bl = 0;
+    for (int32_t v = limb[h]; v; v >>= 1) bl++;
+    int k = h + 1 < 4 ? h + 1 : 4;
+    uint64_t acc = 0;
+    for (int w = h; w > h - k; w--) acc = (acc << 16) | (uint64_t)limb[w];
+    int base = 16 * (h - k + 1);
+    int st = 0;
+    for (int w = h - k; w >= 0; w--) if (limb[w]) { st = 1; break; }
+    *top = acc; *tb = 16 * h + bl - base; *shift = base; *sticky = st;
+    return neg ? -1 : 1;
+}
+
+/* src/fpfixed.c:253-267: round-half-even with a sticky bit. */
+static uint64_t round_sig(uint64_t top, int tb, int bits, int sticky, int *shift)
+{
+    if (tb <= bits) return top;
+    int drop = tb - bits;
+    uint64_t sig = top >> drop;
+    uint64_t rem = top & ((1ULL << drop) - 1);
+    uint64_t half = 1ULL << (drop - 1);
+    int up = rem > half ? 1 : rem < half ? 0 : (sticky ? 1 : (int)(sig & 1));
+    sig += (uint64_t)up;
+    if (sig >> bits) { sig >>= 1; drop++; }
+    *shift += drop;
+    return sig;
+}
+
+/* src/fpfixed.c:269-285: exact zero decodes to +0.0f. */
+void orc_fpx_decode_f32_from(const orc_fpx *c, const int64_t *Cw, float *C)
+{
+    size_t nn = (size_t)c->n * c->n;
+    int32_t *limb = malloc(sizeof(int32_t) * (size_t)(2 * c->L + 2));
+    int S = c->SA + c->SB;
+    if (!limb) return;
+    for (size_t i = 0; i < nn; i++) {
+        uint64_t top; int tb, shift, sticky;
+        int sgn = extract(Cw, c->L, nn, i, limb, &top, &tb, &shift, &sticky);
+        if (!sgn) { C[i] = 0.0f; continue; }
+        uint64_t sig = round_sig(top, tb, 24, sticky, &shift);
+        C[i] = (float)sgn * ldexpf((float)sig, shift - S);
+    }
+    free(limb);
+}
+
+void orc_fpx_decode_f32(const orc_fpx *c, float *C)
+{
+    orc_fpx_decode_f32_from(c, c->Cw, C);
+}
+
+/* src/fpfixed.c:324-328 */
+void orc_fpx_free(orc_fpx *c)
+{
+    free(c->A32); free(c->B32); free(c->Cw);
+    c->A32 = NULL; c->B32 = NULL; c->Cw = NULL;
+}
