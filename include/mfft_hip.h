@@ -1,0 +1,129 @@
+/* mfft_hip.h -- C-ABI shim between the C host API (mfftbench.h) and the
+ * gfx950 HIP kernels of the exact-integer MFFT matrix multiply.
+ *
+ * Plain C types only.  Every entry point returns 0 on success or a negative
+ * MFH_E_* code; on error no output buffer has been written.  A context owns
+ * the device workspace for one (n, L, plan) shape and one HIP stream; it may
+ * be used by one host thread at a time.  Entry points taking host pointers
+ * are synchronous.  Entry points ending in _dev take device pointers, are
+ * ordered on the context's stream and return without synchronising
+ * (mfh_sync() waits).
+ *
+ * Layouts follow the reference (src/mfftbench.h:74-82): a big-integer matrix
+ * is L limb planes, plane u at p[u*n*n + i*n + j], each n x n row-major.
+ * The exact product has RL = 2L+1 uint16 limb planes; the raw convolution
+ * Cw has 2L-1 int64 planes.
+ */
+#ifndef MFFT_HIP_H
+#define MFFT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    MFH_OK = 0,
+    MFH_E_NODEV = -1,    /* no usable gfx950 device                        */
+    MFH_E_NOMEM = -2,    /* device allocation failed                       */
+    MFH_E_ARG = -3,      /* invalid argument (shape, plan, null pointer)   */
+    MFH_E_BOUND = -4,    /* plan/size would overflow a stated accumulator  */
+    MFH_E_RANGE = -5,    /* an input limb lies outside [-65535, 65535]     */
+    MFH_E_HIP = -6,      /* HIP runtime error                              */
+    MFH_E_UNSUPPORTED = -7
+};
+
+/* Input forms accepted by the transform (the limb reader). */
+enum {
+    MFH_IN_U16 = 0,        /* unsigned limbs (the exact track)                */
+    MFH_IN_U16_SIGNED = 1, /* limbs 0..L-2 unsigned, limb L-1 int16: a
+                              two's complement W-bit integer               */
+    MFH_IN_I32 = 2         /* signed int32 limbs, |limb| <= 65535 (conv_mfft) */
+};
+
+typedef struct mfh_ctx mfh_ctx;
+
+/* Flat MFFT plan, the reference's mfft_plan (src/mfftbench.h:139-143). */
+typedef struct {
+    int L, S, NB, K, g;
+    int rec;
+    long long nprod;
+} mfh_plan;
+
+const char *mfh_strerror(int code);
+int  mfh_device_count(void);
+/* gfx arch name of device 0 (e.g. "gfx950"), or "" without a device */
+const char *mfh_device_arch(void);
+
+/* Workspace for products of n x n matrices with L limbs under `plan`.
+ * Rejects plans whose worst case breaks the stated accumulator bounds
+ * (int8 digits, int32 MFMA accumulators, int64 transform values). */
+int  mfh_create(mfh_ctx **ctx, int n, int L, const mfh_plan *plan);
+void mfh_destroy(mfh_ctx *ctx);
+/* device bytes held by the context */
+size_t mfh_workspace_bytes(const mfh_ctx *ctx);
+
+/* ---- host-buffer entry points (synchronous) ----------------------------- */
+/* mm_mfft: exact product of unsigned (or, with MFH_IN_U16_SIGNED, two's
+ * complement) limb matrices into RL >= 2L-1 uint16 planes. */
+int mfh_mm(mfh_ctx *ctx, int in_kind, const uint16_t *A, const uint16_t *B,
+           uint16_t *out, int RL);
+/* conv_mfft: signed int32 limb planes -> 2L-1 int64 coefficient planes. */
+int mfh_conv(mfh_ctx *ctx, const int32_t *A32, const int32_t *B32,
+             int64_t *Cw);
+
+/* ---- device-buffer entry points (stream-ordered, no sync) --------------- */
+int mfh_mm_dev(mfh_ctx *ctx, int in_kind, const void *dA, const void *dB,
+               void *dOut, int RL);
+int mfh_conv_dev(mfh_ctx *ctx, const void *dA32, const void *dB32, void *dCw);
+
+/* fp32 fixed-point embedding on device (src/fpfixed.c semantics):
+ * A, B fp32 n x n; scales 2^SA, 2^SB; product rounded once to fp32. */
+int mfh_fpx_mm_dev(mfh_ctx *ctx, const void *dA, const void *dB, int SA,
+                   int SB, void *dC);
+int mfh_fpx_mm(mfh_ctx *ctx, const float *A, const float *B, int SA, int SB,
+               float *C);
+/* decode only: 2L-1 int64 planes -> fp32 with scale 2^-(SA+SB) (device) */
+int mfh_fpx_decode_dev(mfh_ctx *ctx, const void *dCw, int SAB, void *dC);
+
+/* ---- standalone host-buffer helpers (temporary device buffers) ---------- */
+/* normalize_planes (src/bigmat.c:48-60) on the device */
+int mfh_normalize(const int64_t *acc, int nplanes, int n, uint16_t *out, int RL);
+/* fpx_encode (src/fpfixed.c:175-204) of one fp32 n x n matrix at scale 2^S
+ * into L signed int32 limb planes */
+int mfh_fpx_encode(const float *X, int n, int L, int S, int32_t *X32);
+/* fpx_decode_f32 (src/fpfixed.c:269-285) of 2L-1 int64 planes */
+int mfh_fpx_decode(const int64_t *Cw, int n, int L, int SAB, float *C);
+
+/* ---- device memory and timing helpers ----------------------------------- */
+int  mfh_malloc(void **dptr, size_t bytes);
+int  mfh_free(void *dptr);
+int  mfh_h2d(void *dst, const void *src, size_t bytes);
+int  mfh_d2h(void *dst, const void *src, size_t bytes);
+int  mfh_sync(mfh_ctx *ctx);
+/* bigmat_rand on device: plane-major uint16 limbs from splitmix64(seed),
+ * identical to the host generator (src/bigmat.c:21-35). */
+int  mfh_rand_u16_dev(mfh_ctx *ctx, void *dM, int n, int L, uint64_t seed);
+/* fp32 inputs +-m*2^e (m in [1,2) with 23 random fraction bits, e uniform in
+ * [emin, emax]) from splitmix64(seed), one draw per value. */
+int  mfh_rand_f32_dev(mfh_ctx *ctx, void *dX, size_t count, uint64_t seed,
+                      int emin, int emax);
+
+/* Per-stage device times (ms) of the most recent product on this context,
+ * measured with HIP events on the context's stream:
+ *   [0] transforms in (both operands), [1] pointwise GEMM,
+ *   [2] inverse transform + fold, [3] carry / decode, [4] total.
+ * Timing is recorded only while enabled (it adds event records). */
+int  mfh_set_timing(mfh_ctx *ctx, int enable);
+int  mfh_stage_times(const mfh_ctx *ctx, float ms[5]);
+/* Ops/bytes the kernels are designed to: int8 MFMA ops of the pointwise
+ * GEMM and the minimum HBM bytes of the transform and carry kernels. */
+int  mfh_work(const mfh_ctx *ctx, double *int8_ops, double *fwd_bytes,
+              double *inv_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

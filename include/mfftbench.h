@@ -1,0 +1,115 @@
+/* mfftbench.h -- C host API of the MI355X (gfx950) exact-integer MFFT
+ * matrix multiply.
+ *
+ * Drop-in for the exact-integer path of hadilq/mfft-bench: the functions
+ * below keep the names, signatures, layouts and error conventions of the
+ * reference header src/mfftbench.h (cited per declaration).  The device path
+ * is selected with the extra kernel_t value KERNEL_HIP, so a caller's method
+ * table runs it exactly like the reference's `mfft` rows.  Products run
+ * only on the GPU: this library has no CPU implementation of the product,
+ * and a call that cannot run on the device fails (stderr message, output
+ * untouched, mfft_last_error() < 0) instead of falling back.
+ *
+ * Layout (src/mfftbench.h:74-82): plane-major, p[u*n*n + i*n + j] is limb u
+ * (base 2^16) of entry (i, j).  The exact product has RL = 2L+1 limbs.
+ */
+#ifndef MFFTBENCH_HIP_H
+#define MFFTBENCH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LIMB_BITS 16
+#define LIMB_MASK ((uint32_t)((1u << LIMB_BITS) - 1u))
+
+/* src/mfftbench.h:33-47; KERNEL_HIP appended after the reference's twelve
+ * CPU leaves so their numbering is unchanged. */
+typedef enum {
+    KERNEL_IKJ = 0,
+    KERNEL_BLOCKED,
+    KERNEL_PACKED,
+    KERNEL_STRASSEN,
+    KERNEL_WINOGRAD,
+    KERNEL_BITPLANE,
+    KERNEL_CONVK,
+    KERNEL_CONVKARA,
+    KERNEL_BOOLPACK,
+    KERNEL_BITPACK,
+    KERNEL_BOOLSTRASSEN,
+    KERNEL_BOOLTILED,
+    KERNEL_HIP,          /* gfx950: batched int8 MFMA pointwise GEMM */
+    KERNEL__COUNT
+} kernel_t;
+
+const char *kernel_name(kernel_t k);                 /* src/kernel.c:21-25 */
+int         kernel_from_name(const char *s);         /* src/kernel.c:31-36 */
+
+/* ---- big-integer matrices (src/bigmat.c) -------------------------------- */
+double    now_sec(void);                                         /* :8-13  */
+uint16_t *bigmat_alloc(int n, int L);                            /* :15-18 */
+void      bigmat_rand(uint16_t *m, int n, int L, uint64_t seed); /* :29-35 */
+uint16_t *bigmat_to_entry_major(const uint16_t *plane, int n, int L); /* :37-46 */
+/* :48-60 -- carry-propagates on the device */
+void normalize_planes(const int64_t *acc, int nplanes, int n,
+                      uint16_t *out, int RL);
+int  bigres_equal(const uint16_t *a, const uint16_t *b, int n, int RL,
+                  int *bad_i, int *bad_j, int *bad_w);           /* :62-75 */
+
+/* ---- flat MFFT plan (src/mfftbench.h:139-154, src/mfft.c:77-122) -------- */
+typedef struct {
+    int L, S, NB, K, g;
+    int rec;
+    long long nprod;
+} mfft_plan;
+
+int       mfft_plan_init(mfft_plan *p, int L, int sigma_override);
+long long mfft_plan_products(const mfft_plan *p);
+double    mfft_plan_maxbits(const mfft_plan *p, int n);
+void      mfft_plan_describe(const mfft_plan *p, int n);
+
+/* src/mfftbench.h:156-159, src/mfft.c:302-438.  k must be KERNEL_HIP. */
+void mm_mfft(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
+             const mfft_plan *p, kernel_t k, uint16_t *out, int RL);
+void conv_mfft(int64_t *Cw, const int32_t *A32, const int32_t *B32,
+               int n, int L, const mfft_plan *p, kernel_t k);
+
+/* Two's complement entries (no reference counterpart: the reference's exact
+ * track is unsigned, main.c:3-5, and its conv_mfft takes signed limbs):
+ * limbs 0..L-2 unsigned, limb L-1 read as int16; `out` is the product mod
+ * 2^(16*RL) in two's complement, exact when RL >= 2L+1. */
+void mm_mfft_signed(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
+                    const mfft_plan *p, kernel_t k, uint16_t *out, int RL);
+
+/* ---- fp32 fixed-point embedding (src/mfftbench.h:182-199, src/fpfixed.c) */
+typedef struct {
+    int n, L, sig;
+    int SA, SB;
+    int spreadA, spreadB;
+    int32_t *A32, *B32;     /* signed limb planes, L*n*n each (host)      */
+    int64_t *Cw;            /* exact product, 2L-1 int64 planes (host)    */
+    double enc_secs, dec_secs;
+    void *dev;              /* device copies of A, B (fpx_mm_f32)         */
+} fpx_ctx;
+
+int  fpx_init(fpx_ctx *c, const float *A, const float *B, int n, int force_bits);
+void fpx_encode(fpx_ctx *c, const float *A, const float *B);
+void fpx_decode_f32(fpx_ctx *c, float *C);
+void fpx_free(fpx_ctx *c);
+/* encode -> MFFT product -> decode entirely on the device, from the fp32
+ * matrices given to fpx_encode (no reference counterpart; equals
+ * conv_mfft + fpx_decode_f32 bit for bit). */
+int  fpx_mm_f32(fpx_ctx *c, const mfft_plan *p, float *C);
+
+/* Status of the most recent call on this thread: 0, or a negative code
+ * from mfft_hip.h (MFH_E_*). */
+int         mfft_last_error(void);
+const char *mfft_strerror(int code);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

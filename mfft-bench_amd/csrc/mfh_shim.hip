@@ -1,0 +1,417 @@
+// mfh_shim.hip -- extern "C" entry points of mfft_hip.h: device contexts,
+// workspace, the product pipelines and timing.
+#include <string.h>
+#include <math.h>
+
+#include "mfh_internal.hpp"
+
+namespace {
+
+const char *kErr[] = {"ok",
+                      "no usable gfx950 device",
+                      "device out of memory",
+                      "invalid argument",
+                      "plan or size exceeds a stated accumulator bound",
+                      "input limb outside [-65535, 65535]",
+                      "HIP runtime error",
+                      "unsupported plan"};
+
+char g_arch[64];
+
+int check_device()
+{
+    int cnt = 0;
+    if (hipGetDeviceCount(&cnt) != hipSuccess || cnt < 1) return MFH_E_NODEV;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, 0) != hipSuccess) return MFH_E_NODEV;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return MFH_E_NODEV;
+    return MFH_OK;
+}
+
+int dalloc(mfh_ctx *c, void **p, size_t bytes)
+{
+    *p = nullptr;
+    if (!bytes) return MFH_OK;
+    if (hipMalloc(p, bytes) != hipSuccess) { *p = nullptr; return MFH_E_NOMEM; }
+    c->bytes += bytes;
+    return MFH_OK;
+}
+
+int ensure_staging(mfh_ctx *c, size_t in_bytes, size_t out_bytes)
+{
+    if (c->inBytes < in_bytes) {
+        if (c->dInA) { (void)hipFree(c->dInA); c->bytes -= c->inBytes; }
+        if (c->dInB) { (void)hipFree(c->dInB); c->bytes -= c->inBytes; }
+        c->dInA = c->dInB = nullptr;
+        c->inBytes = 0;
+        int rc = dalloc(c, &c->dInA, in_bytes);
+        if (!rc) rc = dalloc(c, &c->dInB, in_bytes);
+        if (rc) return rc;
+        c->inBytes = in_bytes;
+    }
+    if (c->outBytes < out_bytes) {
+        if (c->dOut) { (void)hipFree(c->dOut); c->bytes -= c->outBytes; }
+        c->dOut = nullptr;
+        c->outBytes = 0;
+        int rc = dalloc(c, &c->dOut, out_bytes);
+        if (rc) return rc;
+        c->outBytes = out_bytes;
+    }
+    return MFH_OK;
+}
+
+void mark(mfh_ctx *c, int k)
+{
+    if (c->timing) (void)hipEventRecord(c->ev[k], c->stream);
+}
+
+// transforms in, pointwise, inverse; leaves the coefficient planes in Cw
+int run_conv(mfh_ctx *c, int kind, const void *dA, const void *dB, int64_t *Cw,
+             int SA, int SB)
+{
+    int rc;
+    mark(c, 0);
+    const int eb = (kind == MFH_IN_U16 || kind == MFH_IN_U16_SIGNED) ? 2 : 4;
+    const int planes = kind == MFH_IN_F32 ? 1 : c->L;
+    if ((rc = mfh_launch_transpose(dB, c->dBt, planes, c->n, eb, c->stream))) return rc;
+    if ((rc = mfh_launch_forward(c, kind, dA, c->dAh, SA))) return rc;
+    if ((rc = mfh_launch_forward(c, kind, c->dBt, c->dBh, SB))) return rc;
+    mark(c, 1);
+    if ((rc = mfh_launch_pointwise(c))) return rc;
+    mark(c, 2);
+    if ((rc = mfh_launch_inverse(c, Cw))) return rc;
+    mark(c, 3);
+    return MFH_OK;
+}
+
+int read_flag(mfh_ctx *c, int *flag)
+{
+    MFH_HIP(hipMemcpyAsync(flag, c->dFlag, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+    MFH_HIP(hipStreamSynchronize(c->stream));
+    return MFH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *mfh_strerror(int code)
+{
+    int k = -code;
+    if (k < 0 || k >= (int)(sizeof kErr / sizeof kErr[0])) return "unknown error";
+    return kErr[k];
+}
+
+int mfh_device_count(void)
+{
+    int cnt = 0;
+    if (hipGetDeviceCount(&cnt) != hipSuccess) return 0;
+    return cnt;
+}
+
+const char *mfh_device_arch(void)
+{
+    g_arch[0] = 0;
+    int cnt = 0;
+    if (hipGetDeviceCount(&cnt) == hipSuccess && cnt > 0) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, 0) == hipSuccess) {
+            strncpy(g_arch, prop.gcnArchName, sizeof g_arch - 1);
+            g_arch[sizeof g_arch - 1] = 0;
+        }
+    }
+    return g_arch;
+}
+
+int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
+{
+    if (!out || !p) return MFH_E_ARG;
+    *out = nullptr;
+    if (n < 1 || L < 2 || (L & (L - 1))) return MFH_E_ARG;
+    // the flat plan of src/mfft.c:77-95
+    if (p->L != L || p->S < 1 || p->NB < 2 || p->K != 2 * p->S ||
+        p->NB * p->S != 2 * L || (2 * p->K) % p->NB || p->g != 2 * p->K / p->NB)
+        return MFH_E_ARG;
+    if (p->K != 4 && p->K != 8 && p->K != 16 && p->K != 32) return MFH_E_UNSUPPORTED;
+    // digit range: |a^| <= (NB/2) * 65535 must fit three balanced int8 digits
+    if ((long long)(p->NB / 2) * 65535 > MFH_DIGIT_MAX) return MFH_E_BOUND;
+    const int np_ = (n + MFH_KBLK - 1) / MFH_KBLK * MFH_KBLK;
+    // int64: NB (inverse) * K * n * ((NB/2) 65535)^2 < 2^62
+    double bits = log2((double)p->NB) + log2((double)p->K) + log2((double)np_) +
+                  2.0 * log2((double)(p->NB / 2) * 65535.0);
+    if (bits >= 62.0) return MFH_E_BOUND;
+    int rc = check_device();
+    if (rc) return rc;
+
+    mfh_ctx *c = new mfh_ctx;
+    memset(c, 0, sizeof *c);
+    c->n = n; c->np = np_; c->L = L; c->S = p->S; c->NB = p->NB; c->K = p->K; c->g = p->g;
+    c->dev = 0;
+    if (hipSetDevice(0) != hipSuccess || hipStreamCreate(&c->stream) != hipSuccess) {
+        delete c;
+        return MFH_E_HIP;
+    }
+    for (int k = 0; k < 5; ++k) (void)hipEventCreate(&c->ev[k]);
+    const size_t nnp = (size_t)np_ * np_, nn = (size_t)n * n;
+    const size_t digit_bytes = (size_t)c->NB * c->K * MFH_DIGITS * nnp;
+    rc = dalloc(c, (void **)&c->dAh, digit_bytes);
+    if (!rc) rc = dalloc(c, (void **)&c->dBh, digit_bytes);
+    if (!rc) rc = dalloc(c, (void **)&c->dCh, (size_t)c->NB * c->K * nnp * sizeof(int64_t));
+    if (!rc) rc = dalloc(c, (void **)&c->dCw, (size_t)(2 * L - 1) * nn * sizeof(int64_t));
+    if (!rc) rc = dalloc(c, &c->dBt, (size_t)L * nn * sizeof(int32_t));
+    if (!rc) rc = dalloc(c, (void **)&c->dFlag, sizeof(int));
+    if (rc) { mfh_destroy(c); return rc; }
+    *out = c;
+    return MFH_OK;
+}
+
+void mfh_destroy(mfh_ctx *c)
+{
+    if (!c) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    void *bufs[] = {c->dAh, c->dBh, c->dCh, c->dCw, c->dBt, c->dFlag,
+                    c->dInA, c->dInB, c->dOut};
+    for (void *b : bufs)
+        if (b) (void)hipFree(b);
+    for (int k = 0; k < 5; ++k)
+        if (c->ev[k]) (void)hipEventDestroy(c->ev[k]);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+size_t mfh_workspace_bytes(const mfh_ctx *c) { return c ? c->bytes : 0; }
+
+int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut, int RL)
+{
+    if (!c || !dA || !dB || !dOut || RL < 1) return MFH_E_ARG;
+    if (kind != MFH_IN_U16 && kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
+    int rc = run_conv(c, kind, dA, dB, c->dCw, 0, 0);
+    if (rc) return rc;
+    if ((rc = mfh_launch_carry(c, c->dCw, (uint16_t *)dOut, RL))) return rc;
+    mark(c, 4);
+    return MFH_OK;
+}
+
+int mfh_conv_dev(mfh_ctx *c, const void *dA32, const void *dB32, void *dCw)
+{
+    if (!c || !dA32 || !dB32 || !dCw) return MFH_E_ARG;
+    int rc, flag = 0;
+    MFH_HIP(hipMemsetAsync(c->dFlag, 0, sizeof(int), c->stream));
+    if ((rc = mfh_launch_check_i32(c, (const int32_t *)dA32, c->L))) return rc;
+    if ((rc = mfh_launch_check_i32(c, (const int32_t *)dB32, c->L))) return rc;
+    if ((rc = read_flag(c, &flag))) return rc;
+    if (flag) return MFH_E_RANGE;
+    rc = run_conv(c, MFH_IN_I32, dA32, dB32, (int64_t *)dCw, 0, 0);
+    if (rc) return rc;
+    mark(c, 4);
+    return MFH_OK;
+}
+
+int mfh_fpx_mm_dev(mfh_ctx *c, const void *dA, const void *dB, int SA, int SB, void *dC)
+{
+    if (!c || !dA || !dB || !dC) return MFH_E_ARG;
+    int rc = run_conv(c, MFH_IN_F32, dA, dB, c->dCw, SA, SB);
+    if (rc) return rc;
+    if ((rc = mfh_launch_decode_f32(c, c->dCw, SA + SB, (float *)dC))) return rc;
+    mark(c, 4);
+    return MFH_OK;
+}
+
+int mfh_fpx_decode_dev(mfh_ctx *c, const void *dCw, int SAB, void *dC)
+{
+    if (!c || !dCw || !dC) return MFH_E_ARG;
+    return mfh_launch_decode_f32(c, (const int64_t *)dCw, SAB, (float *)dC);
+}
+
+int mfh_mm(mfh_ctx *c, int kind, const uint16_t *A, const uint16_t *B, uint16_t *out, int RL)
+{
+    if (!c || !A || !B || !out || RL < 1) return MFH_E_ARG;
+    const size_t nn = (size_t)c->n * c->n;
+    const size_t in_b = (size_t)c->L * nn * 2, out_b = (size_t)RL * nn * 2;
+    int rc = ensure_staging(c, in_b, out_b);
+    if (rc) return rc;
+    MFH_HIP(hipMemcpyAsync(c->dInA, A, in_b, hipMemcpyHostToDevice, c->stream));
+    MFH_HIP(hipMemcpyAsync(c->dInB, B, in_b, hipMemcpyHostToDevice, c->stream));
+    if ((rc = mfh_mm_dev(c, kind, c->dInA, c->dInB, c->dOut, RL))) return rc;
+    MFH_HIP(hipMemcpyAsync(out, c->dOut, out_b, hipMemcpyDeviceToHost, c->stream));
+    MFH_HIP(hipStreamSynchronize(c->stream));
+    return MFH_OK;
+}
+
+int mfh_conv(mfh_ctx *c, const int32_t *A32, const int32_t *B32, int64_t *Cw)
+{
+    if (!c || !A32 || !B32 || !Cw) return MFH_E_ARG;
+    const size_t nn = (size_t)c->n * c->n;
+    const size_t in_b = (size_t)c->L * nn * 4;
+    const size_t out_b = (size_t)(2 * c->L - 1) * nn * 8;
+    int rc = ensure_staging(c, in_b, 0);
+    if (rc) return rc;
+    MFH_HIP(hipMemcpyAsync(c->dInA, A32, in_b, hipMemcpyHostToDevice, c->stream));
+    MFH_HIP(hipMemcpyAsync(c->dInB, B32, in_b, hipMemcpyHostToDevice, c->stream));
+    if ((rc = mfh_conv_dev(c, c->dInA, c->dInB, c->dCw))) return rc;
+    MFH_HIP(hipMemcpyAsync(Cw, c->dCw, out_b, hipMemcpyDeviceToHost, c->stream));
+    MFH_HIP(hipStreamSynchronize(c->stream));
+    return MFH_OK;
+}
+
+int mfh_fpx_mm(mfh_ctx *c, const float *A, const float *B, int SA, int SB, float *C)
+{
+    if (!c || !A || !B || !C) return MFH_E_ARG;
+    const size_t nn = (size_t)c->n * c->n;
+    int rc = ensure_staging(c, nn * 4, nn * 4);
+    if (rc) return rc;
+    MFH_HIP(hipMemcpyAsync(c->dInA, A, nn * 4, hipMemcpyHostToDevice, c->stream));
+    MFH_HIP(hipMemcpyAsync(c->dInB, B, nn * 4, hipMemcpyHostToDevice, c->stream));
+    if ((rc = mfh_fpx_mm_dev(c, c->dInA, c->dInB, SA, SB, c->dOut))) return rc;
+    MFH_HIP(hipMemcpyAsync(C, c->dOut, nn * 4, hipMemcpyDeviceToHost, c->stream));
+    MFH_HIP(hipStreamSynchronize(c->stream));
+    return MFH_OK;
+}
+
+int mfh_malloc(void **p, size_t bytes)
+{
+    if (!p) return MFH_E_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    if (hipMalloc(p, bytes) != hipSuccess) { *p = nullptr; return MFH_E_NOMEM; }
+    return MFH_OK;
+}
+
+int mfh_free(void *p)
+{
+    MFH_HIP(hipFree(p));
+    return MFH_OK;
+}
+
+int mfh_h2d(void *dst, const void *src, size_t bytes)
+{
+    MFH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return MFH_OK;
+}
+
+int mfh_d2h(void *dst, const void *src, size_t bytes)
+{
+    MFH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+
+int mfh_sync(mfh_ctx *c)
+{
+    if (c) MFH_HIP(hipStreamSynchronize(c->stream));
+    else MFH_HIP(hipDeviceSynchronize());
+    return MFH_OK;
+}
+
+int mfh_rand_u16_dev(mfh_ctx *c, void *dM, int n, int L, uint64_t seed)
+{
+    if (!dM || n < 1 || L < 1) return MFH_E_ARG;
+    return mfh_launch_rand_u16(dM, (size_t)L * n * n, seed, c ? c->stream : 0);
+}
+
+int mfh_rand_f32_dev(mfh_ctx *c, void *dX, size_t count, uint64_t seed, int emin, int emax)
+{
+    if (!dX) return MFH_E_ARG;
+    return mfh_launch_rand_f32(dX, count, seed, emin, emax, c ? c->stream : 0);
+}
+
+int mfh_set_timing(mfh_ctx *c, int enable)
+{
+    if (!c) return MFH_E_ARG;
+    c->timing = enable ? 1 : 0;
+    return MFH_OK;
+}
+
+int mfh_stage_times(const mfh_ctx *c, float ms[5])
+{
+    if (!c || !ms) return MFH_E_ARG;
+    MFH_HIP(hipEventSynchronize(c->ev[4]));
+    for (int k = 0; k < 4; ++k) MFH_HIP(hipEventElapsedTime(&ms[k], c->ev[k], c->ev[k + 1]));
+    MFH_HIP(hipEventElapsedTime(&ms[4], c->ev[0], c->ev[4]));
+    return MFH_OK;
+}
+
+int mfh_work(const mfh_ctx *c, double *ops, double *fwd, double *inv)
+{
+    if (!c) return MFH_E_ARG;
+    const double nnp = (double)c->np * c->np, nn = (double)c->n * c->n;
+    const double pts = (double)c->NB * c->K;
+    if (ops) *ops = 2.0 * MFH_DIGITS * MFH_DIGITS * c->NB * (double)c->K * c->K * nnp * c->np;
+    if (fwd) *fwd = 2.0 * ((double)c->L * nn * 2.0 + pts * MFH_DIGITS * nnp);
+    if (inv) *inv = pts * nnp * 8.0 + (2.0 * c->L - 1.0) * nn * 8.0;
+    return MFH_OK;
+}
+
+}  // extern "C"
+
+// standalone helpers: a throw-away context carrying only sizes and the null
+// stream, with temporary device buffers
+namespace {
+struct TmpBufs {
+    void *p[3] = {nullptr, nullptr, nullptr};
+    ~TmpBufs() { for (void *q : p) if (q) (void)hipFree(q); }
+};
+void bare_ctx(mfh_ctx &c, int n, int L)
+{
+    memset(&c, 0, sizeof c);
+    c.n = n; c.np = n; c.L = L; c.stream = 0;
+}
+}  // namespace
+
+extern "C" {
+
+int mfh_normalize(const int64_t *acc, int nplanes, int n, uint16_t *out, int RL)
+{
+    if (!acc || !out || n < 1 || nplanes < 0 || RL < 1) return MFH_E_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t nn = (size_t)n * n;
+    TmpBufs t;
+    if (hipMalloc(&t.p[0], (size_t)(nplanes ? nplanes : 1) * nn * 8) != hipSuccess ||
+        hipMalloc(&t.p[1], (size_t)RL * nn * 2) != hipSuccess)
+        return MFH_E_NOMEM;
+    MFH_HIP(hipMemcpy(t.p[0], acc, (size_t)nplanes * nn * 8, hipMemcpyHostToDevice));
+    if ((rc = mfh_launch_carry_planes((const int64_t *)t.p[0], nplanes, nn,
+                                      (uint16_t *)t.p[1], RL, 0)))
+        return rc;
+    MFH_HIP(hipMemcpy(out, t.p[1], (size_t)RL * nn * 2, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+
+int mfh_fpx_encode(const float *X, int n, int L, int S, int32_t *X32)
+{
+    if (!X || !X32 || n < 1 || L < 1) return MFH_E_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t nn = (size_t)n * n;
+    TmpBufs t;
+    if (hipMalloc(&t.p[0], nn * 4) != hipSuccess ||
+        hipMalloc(&t.p[1], (size_t)L * nn * 4) != hipSuccess)
+        return MFH_E_NOMEM;
+    MFH_HIP(hipMemcpy(t.p[0], X, nn * 4, hipMemcpyHostToDevice));
+    if ((rc = mfh_launch_encode_f32((const float *)t.p[0], n, L, S, (int32_t *)t.p[1], 0)))
+        return rc;
+    MFH_HIP(hipMemcpy(X32, t.p[1], (size_t)L * nn * 4, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+
+int mfh_fpx_decode(const int64_t *Cw, int n, int L, int SAB, float *C)
+{
+    if (!Cw || !C || n < 1 || L < 1) return MFH_E_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t nn = (size_t)n * n;
+    TmpBufs t;
+    if (hipMalloc(&t.p[0], (size_t)(2 * L - 1) * nn * 8) != hipSuccess ||
+        hipMalloc(&t.p[1], nn * 4) != hipSuccess)
+        return MFH_E_NOMEM;
+    MFH_HIP(hipMemcpy(t.p[0], Cw, (size_t)(2 * L - 1) * nn * 8, hipMemcpyHostToDevice));
+    mfh_ctx c;
+    bare_ctx(c, n, L);
+    if ((rc = mfh_launch_decode_f32(&c, (const int64_t *)t.p[0], SAB, (float *)t.p[1])))
+        return rc;
+    MFH_HIP(hipDeviceSynchronize());
+    MFH_HIP(hipMemcpy(C, t.p[1], nn * 4, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+
+}  // extern "C"

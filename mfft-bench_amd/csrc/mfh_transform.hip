@@ -1,0 +1,510 @@
+// mfh_transform.hip -- bandwidth-side kernels of the gfx950 MFFT matmul:
+// forward ring transform with digit split, inverse transform + fold, carry
+// normalisation, fp32 decode, plane transpose and seeded input generators.
+//
+// Ring R = Z[y]/(y^K + 1); omega = y^g is a primitive NB-th root of unity
+// (g = 2K/NB).  A matrix element's L limbs form NB/2 non-zero blocks of S
+// limbs (block b holds limbs b*S .. b*S+S-1 in ring coefficients 0..S-1,
+// src/mfft.c:322-336); its transform is
+//     X[j] = sum_b omega^(j*b) x_b,   j = 0 .. NB-1   (natural order).
+// Multiplying by y^e is a negacyclic shift, so every output coefficient is
+// a signed sum of input limbs: no multiplications anywhere.
+#include "mfh_internal.hpp"
+
+namespace {
+
+// ---- limb readers -----------------------------------------------------------
+struct SrcU16 {
+    const uint16_t *p;
+    size_t nn;
+    int n, L;
+    __device__ int get(int u, int i, int k) const
+    {
+        return p[(size_t)u * nn + (size_t)i * n + k];
+    }
+};
+
+// two's complement W-bit integers: the top limb is signed
+struct SrcU16Signed {
+    const uint16_t *p;
+    size_t nn;
+    int n, L;
+    __device__ int get(int u, int i, int k) const
+    {
+        uint16_t v = p[(size_t)u * nn + (size_t)i * n + k];
+        return u == L - 1 ? (int)(int16_t)v : (int)v;
+    }
+};
+
+struct SrcI32 {
+    const int32_t *p;
+    size_t nn;
+    int n, L;
+    __device__ int get(int u, int i, int k) const
+    {
+        return p[(size_t)u * nn + (size_t)i * n + k];
+    }
+};
+
+// fp32 on a fixed-point grid of scale 2^S (src/fpfixed.c:175-193): limb u
+// of x * 2^S, as a signed limb.  frexp gives x = m 2^e, mi = |m| 2^24 is an
+// exact 24-bit integer, and the value mi << (e - 24 + S) lands in limbs
+// lo .. lo+2 with lo = (e-24+S) >> 4.
+struct SrcF32 {
+    const float *p;
+    size_t nn;
+    int n, L, S;
+    __device__ int get(int u, int i, int k) const
+    {
+        float x = p[(size_t)i * n + k];
+        if (x == 0.0f || !isfinite(x)) return 0;
+        int e;
+        float m = frexpf(x, &e);
+        int mi = (int)(fabsf(m) * 16777216.0f);
+        int off = e - 24 + S;
+        if (off < 0) return 0;
+        int lo = off >> 4, t = u - lo;
+        if (t < 0 || t > 2) return 0;
+        unsigned long long v = (unsigned long long)mi << (off & 15);
+        int limb = (int)((v >> (16 * t)) & 0xFFFFu);
+        return x < 0.0f ? -limb : limb;
+    }
+};
+
+__device__ __forceinline__ void split3(int v, int &d0, int &d1, int &d2)
+{
+    d0 = (v << 24) >> 24;          // sign-extended low byte
+    int v1 = (v - d0) >> 8;        // exact
+    d1 = (v1 << 24) >> 24;
+    d2 = (v1 - d1) >> 8;           // in [-128, 127] by the plan bound
+}
+
+// ---- forward transform, generic plan ---------------------------------------
+// One thread per padded element (i, k) of an np x np operand; it writes the
+// three digit planes of every (point j, coefficient c).  Elements outside
+// the n x n input are zero.  Output plane (j, c, r) holds digit r of X[j][c]
+// as an np x np row-major int8 matrix.
+template <class Src>
+__global__ __launch_bounds__(256) void k_forward_generic(
+    Src src, int8_t *__restrict__ out, int np_, int LS, int S, int NB, int K,
+    int g)
+{
+    const size_t nnp = (size_t)np_ * np_;
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= nnp) return;
+    const int i = (int)(e / np_), k = (int)(e % np_);
+    const bool valid = i < src.n && k < src.n;
+    const int twoK = 2 * K;
+    for (int j = 0; j < NB; ++j) {
+        for (int c = 0; c < K; ++c) {
+            int acc = 0;
+            if (valid) {
+                for (int b = 0; b < LS; ++b) {
+                    int ejb = (g * j * b) % twoK;
+                    int s = c - ejb;
+                    if (s < 0) s += twoK;
+                    if (s < S) acc += src.get(b * S + s, i, k);
+                    else if (s >= K && s < K + S) acc -= src.get(b * S + s - K, i, k);
+                }
+            }
+            int d0, d1, d2;
+            split3(acc, d0, d1, d2);
+            int8_t *o = out + ((size_t)(j * K + c) * MFH_DIGITS) * nnp + e;
+            o[0] = (int8_t)d0;
+            o[nnp] = (int8_t)d1;
+            o[2 * nnp] = (int8_t)d2;
+        }
+    }
+}
+
+// |limb| <= 65535 for int32 inputs (the transform and digit bounds assume it)
+__global__ __launch_bounds__(256) void k_check_i32(const int32_t *p, size_t count,
+                                                   int *flag)
+{
+    size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * 256;
+    bool bad = false;
+    for (; idx < count; idx += stride) {
+        int v = p[idx];
+        bad |= (v > 65535) || (v < -65535);
+    }
+    if (bad) atomicOr(flag, 1);
+}
+
+// ---- inverse transform + /NB + fold -----------------------------------------
+// One workgroup holds `epw` elements, each with NB*K int64 values, twice
+// (ping-pong) in LDS; thread (le, c) owns ring coefficient c of element le.
+// Input C^[j][i][j'][c] in natural point order is loaded bit-reversed, then
+// Cooley-Tukey stages len = 2..NB with conjugate twiddles give NB * x_b in
+// natural order (the semantics of src/mfft.c:260-299).  Fold:
+//     Cw[b*S + c] = x_b[c] + x_(b-1)[c + S],  c < S   (src/mfft.c:407-418)
+__global__ void k_inverse_fold(const int64_t *__restrict__ Ch,
+                               int64_t *__restrict__ Cw, int n, int np_,
+                               int NB, int K, int S, int g, int lgNB, int P,
+                               int epw)
+{
+    extern __shared__ int64_t sm[];
+    const int tid = threadIdx.x;
+    const int le = tid / K, c = tid % K;
+    const size_t nn = (size_t)n * n;
+    const size_t e = (size_t)blockIdx.x * epw + le;
+    const bool valid = le < epw && e < nn;
+    const int blk = NB * K;
+    int64_t *X = sm + (size_t)le * blk;
+    int64_t *Y = sm + (size_t)epw * blk + (size_t)le * blk;
+    const int i = valid ? (int)(e / n) : 0, jj = valid ? (int)(e % n) : 0;
+    if (valid) {
+        for (int j = 0; j < NB; ++j) {
+            const int r = lgNB ? (int)(__brev((unsigned)j) >> (32 - lgNB)) : 0;
+            X[r * K + c] = Ch[(((size_t)j * np_ + i) * np_ + jj) * K + c];
+        }
+    }
+    __syncthreads();
+    const int twoK = 2 * K;
+    for (int len = 2; len <= NB; len <<= 1) {
+        const int h = len >> 1, step = NB / len;
+        if (valid) {
+            for (int j0 = 0; j0 < NB; j0 += len)
+                for (int t = 0; t < h; ++t) {
+                    const int p = j0 + t, q = p + h;
+                    const int ex = (g * t * step) % twoK;
+                    int s = c + ex;                   // (y^-ex v)[c] = v[c+ex]
+                    if (s >= twoK) s -= twoK;
+                    int64_t w = s < K ? X[q * K + s] : -X[q * K + s - K];
+                    int64_t u = X[p * K + c];
+                    Y[p * K + c] = u + w;
+                    Y[q * K + c] = u - w;
+                }
+        }
+        __syncthreads();
+        int64_t *tmp = X; X = Y; Y = tmp;
+    }
+    if (valid && c < S) {
+        for (int b = 0; b < NB; ++b) {
+            const int w = b * S + c;
+            if (w >= P) break;
+            int64_t v = X[b * K + c] >> lgNB;            // exact multiples of NB
+            if (b > 0) v += X[(b - 1) * K + c + S] >> lgNB;
+            Cw[(size_t)w * nn + e] = v;
+        }
+    }
+}
+
+// ---- carry normalisation (src/bigmat.c:48-60) ------------------------------
+__global__ __launch_bounds__(256) void k_carry(const int64_t *__restrict__ Cw,
+                                               uint16_t *__restrict__ out,
+                                               size_t nn, int P, int RL)
+{
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= nn) return;
+    int64_t carry = 0;
+    for (int w = 0; w < RL; ++w) {
+        int64_t v = carry + (w < P ? Cw[(size_t)w * nn + e] : 0);
+        out[(size_t)w * nn + e] = (uint16_t)(v & 0xFFFF);
+        carry = v >> 16;
+    }
+}
+
+// ---- fp32 decode (src/fpfixed.c:212-285) --------------------------------------
+// Carry over RL = 2L+2 limbs with an arithmetic shift, take the magnitude
+// (two's complement negation when the final carry is negative), keep the
+// top <= 4 limbs below the highest non-zero one plus a sticky bit, round to
+// 24 bits half-even, and scale by 2^-(SA+SB).  Exact zero gives +0.0f.
+// Streaming: both the value and its negation are tracked limb by limb, so no
+// per-element limb array is needed.
+struct TopTrack {
+    int h;
+    uint32_t hist[4];      // limbs w-3 .. w
+    uint32_t win[4];       // limbs h-3 .. h when h was set
+    uint32_t below;        // OR of limbs < w-3
+    uint32_t sticky;       // OR of limbs < h-3 when h was set
+    __device__ void init()
+    {
+        h = -1; below = 0; sticky = 0;
+        for (int q = 0; q < 4; ++q) { hist[q] = 0; win[q] = 0; }
+    }
+    __device__ void push(int w, uint32_t limb)
+    {
+        below |= hist[0];
+        hist[0] = hist[1]; hist[1] = hist[2]; hist[2] = hist[3]; hist[3] = limb;
+        if (limb) {
+            h = w;
+            for (int q = 0; q < 4; ++q) win[q] = hist[q];
+            sticky = below;
+        }
+    }
+};
+
+__global__ __launch_bounds__(256) void k_decode_f32(const int64_t *__restrict__ Cw,
+                                                    float *__restrict__ out,
+                                                    size_t nn, int P, int RL,
+                                                    int SAB)
+{
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= nn) return;
+    TopTrack pos, neg;
+    pos.init(); neg.init();
+    int64_t carry = 0;
+    uint32_t borrow = 1;
+    for (int w = 0; w < RL; ++w) {
+        int64_t t = carry + (w < P ? Cw[(size_t)w * nn + e] : 0);
+        uint32_t limb = (uint32_t)(t & 0xFFFF);
+        carry = t >> 16;
+        uint32_t nl = ((~limb) & 0xFFFFu) + borrow;
+        borrow = nl >> 16;
+        nl &= 0xFFFFu;
+        pos.push(w, limb);
+        neg.push(w, nl);
+    }
+    const bool isneg = carry < 0;
+    const int h = isneg ? neg.h : pos.h;
+    if (h < 0) { out[e] = 0.0f; return; }
+    uint32_t win[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) win[q] = isneg ? neg.win[q] : pos.win[q];
+    const uint32_t sticky = isneg ? neg.sticky : pos.sticky;
+    int bl = 32 - __clz(win[3]);
+    const int k = h + 1 < 4 ? h + 1 : 4;
+    unsigned long long top = 0;
+#pragma unroll
+    for (int q = 3; q >= 0; --q)
+        if (q > 3 - k) top = (top << 16) | win[q];
+    // limbs below the gathered ones: win[0 .. 3-k] (positions h-3 .. h-k)
+    // only exist when k == 4, so sticky is the OR below h-3.
+    const int base = 16 * (h - k + 1);
+    int tb = 16 * h + bl - base;
+    int shift = base;
+    unsigned long long sig = top;
+    if (tb > 24) {
+        int drop = tb - 24;
+        sig = top >> drop;
+        unsigned long long rem = top & ((1ULL << drop) - 1);
+        unsigned long long half = 1ULL << (drop - 1);
+        int up = rem > half ? 1 : rem < half ? 0 : (sticky ? 1 : (int)(sig & 1));
+        sig += (unsigned long long)up;
+        if (sig >> 24) { sig >>= 1; drop++; }
+        shift += drop;
+    }
+    float v = ldexpf((float)sig, shift - SAB);
+    out[e] = isneg ? -v : v;
+}
+
+// ---- fp32 encode into limb planes (src/fpfixed.c:175-204) -------------------
+__global__ __launch_bounds__(256) void k_encode_f32(SrcF32 src, int32_t *__restrict__ out)
+{
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= src.nn) return;
+    const int i = (int)(e / src.n), k = (int)(e % src.n);
+    for (int u = 0; u < src.L; ++u) out[(size_t)u * src.nn + e] = src.get(u, i, k);
+}
+
+// ---- plane transpose (B operand) -----------------------------------------------
+template <class T>
+__global__ __launch_bounds__(256) void k_transpose(const T *__restrict__ src,
+                                                   T *__restrict__ dst, int n)
+{
+    __shared__ T tile[64][65];
+    const size_t nn = (size_t)n * n;
+    const T *s = src + (size_t)blockIdx.z * nn;
+    T *d = dst + (size_t)blockIdx.z * nn;
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+    for (int r = ty; r < 64; r += 4) {
+        int rr = r0 + r, cc = c0 + tx;
+        if (rr < n && cc < n) tile[r][tx] = s[(size_t)rr * n + cc];
+    }
+    __syncthreads();
+    for (int r = ty; r < 64; r += 4) {
+        int rr = c0 + r, cc = r0 + tx;     // dst row = src col
+        if (rr < n && cc < n) d[(size_t)rr * n + cc] = tile[tx][r];
+    }
+}
+
+// ---- seeded generators (splitmix64: output i is mix(seed + (i+1) gamma)) ----
+__device__ __forceinline__ uint64_t sm64_mix(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void k_rand_u16(uint16_t *dst, size_t count,
+                                                  uint64_t seed)
+{
+    size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * 256;
+    for (; idx < count; idx += stride)
+        dst[idx] = (uint16_t)sm64_mix(seed + (uint64_t)(idx + 1) * 0x9E3779B97F4A7C15ULL);
+}
+
+__global__ __launch_bounds__(256) void k_rand_f32(float *dst, size_t count,
+                                                  uint64_t seed, int emin,
+                                                  unsigned span)
+{
+    size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * 256;
+    for (; idx < count; idx += stride) {
+        uint64_t u = sm64_mix(seed + (uint64_t)(idx + 1) * 0x9E3779B97F4A7C15ULL);
+        float m = 1.0f + (float)((u >> 40) & 0x7FFFFFu) * (1.0f / 8388608.0f);
+        int e = emin + (int)(u % span);
+        float x = ldexpf(m, e);
+        dst[idx] = (u >> 63) ? -x : x;
+    }
+}
+
+int lg2i(int x) { int r = 0; while ((1 << r) < x) ++r; return r; }
+
+unsigned grid_for(size_t count, unsigned cap)
+{
+    size_t g = (count + 255) / 256;
+    if (g > cap) g = cap;
+    return g ? (unsigned)g : 1u;
+}
+
+}  // namespace
+
+// ============================================================================
+int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
+                         int elem_bytes, hipStream_t st)
+{
+    dim3 grid((n + 63) / 64, (n + 63) / 64, planes);
+    if (elem_bytes == 2)
+        hipLaunchKernelGGL(k_transpose<uint16_t>, grid, dim3(256), 0, st,
+                           (const uint16_t *)src, (uint16_t *)dst, n);
+    else if (elem_bytes == 4)
+        hipLaunchKernelGGL(k_transpose<uint32_t>, grid, dim3(256), 0, st,
+                           (const uint32_t *)src, (uint32_t *)dst, n);
+    else
+        return MFH_E_ARG;
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
+                       int scale_S)
+{
+    const size_t nnp = (size_t)c->np * c->np;
+    const size_t nn = (size_t)c->n * c->n;
+    dim3 grid((unsigned)((nnp + 255) / 256));
+    const int LS = c->L / c->S;
+    switch (in_kind) {
+    case MFH_IN_U16: {
+        SrcU16 s{(const uint16_t *)src, nn, c->n, c->L};
+        hipLaunchKernelGGL(k_forward_generic<SrcU16>, grid, dim3(256), 0, c->stream,
+                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+        break;
+    }
+    case MFH_IN_U16_SIGNED: {
+        SrcU16Signed s{(const uint16_t *)src, nn, c->n, c->L};
+        hipLaunchKernelGGL(k_forward_generic<SrcU16Signed>, grid, dim3(256), 0,
+                           c->stream, s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+        break;
+    }
+    case MFH_IN_I32: {
+        SrcI32 s{(const int32_t *)src, nn, c->n, c->L};
+        hipLaunchKernelGGL(k_forward_generic<SrcI32>, grid, dim3(256), 0, c->stream,
+                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+        break;
+    }
+    case MFH_IN_F32: {
+        SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
+        hipLaunchKernelGGL(k_forward_generic<SrcF32>, grid, dim3(256), 0, c->stream,
+                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+        break;
+    }
+    default:
+        return MFH_E_ARG;
+    }
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_check_i32(mfh_ctx *c, const int32_t *src, int planes)
+{
+    size_t count = (size_t)planes * c->n * c->n;
+    hipLaunchKernelGGL(k_check_i32, dim3(grid_for(count, 4096)), dim3(256), 0,
+                       c->stream, src, count, c->dFlag);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw)
+{
+    const int blk = c->NB * c->K;
+    int epw = 8192 / blk;              // 2 * epw * blk * 8 bytes <= 128 KiB
+    if (epw > 64) epw = 64;
+    if (epw < 1) return MFH_E_UNSUPPORTED;
+    int threads = epw * c->K;
+    if (threads > 1024) { epw = 1024 / c->K; threads = epw * c->K; }
+    if (threads < 64) threads = 64;    // keep whole waves; extra threads idle
+    const size_t nn = (size_t)c->n * c->n;
+    const size_t lds = (size_t)2 * epw * blk * sizeof(int64_t);
+    static bool attr_set = false;
+    if (!attr_set) {
+        MFH_HIP(hipFuncSetAttribute((const void *)k_inverse_fold,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 131072));
+        attr_set = true;
+    }
+    dim3 grid((unsigned)((nn + epw - 1) / epw));
+    hipLaunchKernelGGL(k_inverse_fold, grid, dim3(threads), lds, c->stream,
+                       c->dCh, Cw, c->n, c->np, c->NB, c->K, c->S, c->g,
+                       lg2i(c->NB), 2 * c->L - 1, epw);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_carry(mfh_ctx *c, const int64_t *Cw, uint16_t *out, int RL)
+{
+    const size_t nn = (size_t)c->n * c->n;
+    hipLaunchKernelGGL(k_carry, dim3((unsigned)((nn + 255) / 256)), dim3(256), 0,
+                       c->stream, Cw, out, nn, 2 * c->L - 1, RL);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_carry_planes(const int64_t *Cw, int P, size_t nn, uint16_t *out,
+                            int RL, hipStream_t st)
+{
+    hipLaunchKernelGGL(k_carry, dim3((unsigned)((nn + 255) / 256)), dim3(256), 0, st,
+                       Cw, out, nn, P, RL);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_encode_f32(const float *X, int n, int L, int S, int32_t *out,
+                          hipStream_t st)
+{
+    const size_t nn = (size_t)n * n;
+    SrcF32 s{X, nn, n, L, S};
+    hipLaunchKernelGGL(k_encode_f32, dim3((unsigned)((nn + 255) / 256)), dim3(256), 0, st,
+                       s, out);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_decode_f32(mfh_ctx *c, const int64_t *Cw, int SAB, float *out)
+{
+    const size_t nn = (size_t)c->n * c->n;
+    hipLaunchKernelGGL(k_decode_f32, dim3((unsigned)((nn + 255) / 256)), dim3(256),
+                       0, c->stream, Cw, out, nn, 2 * c->L - 1, 2 * c->L + 2, SAB);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_rand_u16(void *dst, size_t count, uint64_t seed, hipStream_t st)
+{
+    hipLaunchKernelGGL(k_rand_u16, dim3(grid_for(count, 65536)), dim3(256), 0, st,
+                       (uint16_t *)dst, count, seed);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_rand_f32(void *dst, size_t count, uint64_t seed, int emin,
+                        int emax, hipStream_t st)
+{
+    if (emax < emin) return MFH_E_ARG;
+    hipLaunchKernelGGL(k_rand_f32, dim3(grid_for(count, 65536)), dim3(256), 0, st,
+                       (float *)dst, count, seed, emin, (unsigned)(emax - emin + 1));
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}

@@ -1,0 +1,313 @@
+/* mfftbench_api.c -- the reference-named C API (include/mfftbench.h) over
+ * the gfx950 shim (include/mfft_hip.h).
+ *
+ * Products run only on the device.  Errors follow the reference's
+ * conventions (src/mfft.c:317-320, 432): a message on stderr and the output
+ * left untouched; the code is kept for mfft_last_error().  Each call owns
+ * nothing between calls except one cached device context per thread-free
+ * process-wide slot (keyed by n, L and the plan), which saves re-allocating
+ * the workspace when a caller repeats a shape. */
+#define _GNU_SOURCE
+#include <math.h>
+#include <pthread.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#include "mfft_hip.h"
+#include "mfftbench.h"
+
+static __thread int t_last_error;
+static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
+static mfh_ctx *g_ctx;
+static int g_key[4];
+
+int mfft_last_error(void) { return t_last_error; }
+const char *mfft_strerror(int code) { return mfh_strerror(code); }
+
+static int fail(const char *what, int code)
+{
+    t_last_error = code;
+    fprintf(stderr, "mfft-hip: %s: %s\n", what, mfh_strerror(code));
+    return code;
+}
+
+/* src/kernel.c:16-36 */
+static const char *knames[KERNEL__COUNT] = {
+    "ikj", "blocked", "packed", "strassen", "winograd", "bitplane",
+    "convk", "convkara", "boolpack", "bitpack", "boolstrassen", "booltiled",
+    "hip"};
+
+const char *kernel_name(kernel_t k)
+{
+    if ((int)k < 0 || k >= KERNEL__COUNT) return "?";
+    return knames[k];
+}
+
+int kernel_from_name(const char *s)
+{
+    for (int i = 0; i < KERNEL__COUNT; i++)
+        if (strcmp(s, knames[i]) == 0) return i;
+    return -1;
+}
+
+/* ---- src/bigmat.c ------------------------------------------------------ */
+double now_sec(void)
+{
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + (double)ts.tv_nsec * 1e-9;
+}
+
+uint16_t *bigmat_alloc(int n, int L)
+{
+    return calloc((size_t)n * n * (size_t)L, sizeof(uint16_t));
+}
+
+/* SplitMix64 inputs, plane-major (src/bigmat.c:21-35).  Input generation,
+ * not part of the product path. */
+void bigmat_rand(uint16_t *m, int n, int L, uint64_t seed)
+{
+    uint64_t s = seed;
+    size_t total = (size_t)n * n * (size_t)L;
+    for (size_t i = 0; i < total; i++) {
+        s += 0x9E3779B97F4A7C15ULL;
+        uint64_t z = s;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+        m[i] = (uint16_t)(z ^ (z >> 31));
+    }
+}
+
+uint16_t *bigmat_to_entry_major(const uint16_t *plane, int n, int L)
+{
+    uint16_t *e = bigmat_alloc(n, L);
+    if (!e) return NULL;
+    size_t nn = (size_t)n * n;
+    for (int u = 0; u < L; u++)
+        for (size_t idx = 0; idx < nn; idx++) e[idx * L + u] = plane[(size_t)u * nn + idx];
+    return e;
+}
+
+void normalize_planes(const int64_t *acc, int nplanes, int n, uint16_t *out, int RL)
+{
+    int rc = mfh_normalize(acc, nplanes, n, out, RL);
+    t_last_error = rc;
+    if (rc) fail("normalize_planes", rc);
+}
+
+int bigres_equal(const uint16_t *a, const uint16_t *b, int n, int RL,
+                 int *bad_i, int *bad_j, int *bad_w)
+{
+    size_t nn = (size_t)n * n;
+    for (int w = 0; w < RL; w++)
+        for (size_t idx = 0; idx < nn; idx++)
+            if (a[(size_t)w * nn + idx] != b[(size_t)w * nn + idx]) {
+                if (bad_w) *bad_w = w;
+                if (bad_i) *bad_i = (int)(idx / (size_t)n);
+                if (bad_j) *bad_j = (int)(idx % (size_t)n);
+                return 0;
+            }
+    return 1;
+}
+
+/* ---- plan (src/mfft.c:75-122) ------------------------------------------- */
+static int ilog2i(int x) { int r = 0; while ((1 << r) < x) r++; return r; }
+
+int mfft_plan_init(mfft_plan *p, int L, int sigma_override)
+{
+    if (L < 2 || (L & (L - 1))) return -1;
+    int l = ilog2i(L);
+    int sigma = sigma_override > 0 ? sigma_override : l / 2;
+    if (sigma < 1) sigma = 1;
+    if (sigma > l) return -1;
+    int S = 1 << sigma, NB = 2 * L / S, K = 2 * S;
+    if (2 * S * S < L || (2 * K) % NB || NB < 2) return -1;
+    p->L = L; p->S = S; p->NB = NB; p->K = K; p->g = 2 * K / NB;
+    p->rec = 0;
+    p->nprod = (long long)NB * K * K;
+    return 0;
+}
+
+long long mfft_plan_products(const mfft_plan *p)
+{
+    return p->nprod ? p->nprod : (long long)p->NB * p->K * p->K;
+}
+
+double mfft_plan_maxbits(const mfft_plan *p, int n)
+{
+    return 3.0 * log2((double)p->NB) + log2((double)p->K) + log2((double)n) +
+           2.0 * LIMB_BITS;
+}
+
+void mfft_plan_describe(const mfft_plan *p, int n)
+{
+    printf("MFFT plan: L=%d limbs per entry (scalar width %d bits)  S=%d  "
+           "NB=%d  K=%d  omega=I_%d^%d\n",
+           p->L, p->L * LIMB_BITS, p->S, p->NB, p->K, ilog2i(p->K), p->g);
+    printf("           n x n matrix products: MFFT %lld vs limb-plane %d "
+           "(ratio %.2fx)  worst-case %.0f bits\n",
+           mfft_plan_products(p), p->L * p->L,
+           (double)(p->L * p->L) / (double)mfft_plan_products(p),
+           mfft_plan_maxbits(p, n));
+}
+
+/* ---- device context cache ------------------------------------------------ */
+static int get_ctx(int n, int L, const mfft_plan *p, mfh_ctx **out)
+{
+    if (!p || p->rec) return MFH_E_ARG;
+    int key[4] = {n, L, p->S, p->NB};
+    if (g_ctx && memcmp(key, g_key, sizeof key) == 0) { *out = g_ctx; return 0; }
+    if (g_ctx) { mfh_destroy(g_ctx); g_ctx = NULL; }
+    mfh_plan hp = {p->L, p->S, p->NB, p->K, p->g, 0, p->nprod};
+    int rc = mfh_create(&g_ctx, n, L, &hp);
+    if (rc) { g_ctx = NULL; return rc; }
+    memcpy(g_key, key, sizeof key);
+    *out = g_ctx;
+    return 0;
+}
+
+static void mm_common(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
+                      const mfft_plan *p, kernel_t k, uint16_t *out, int RL,
+                      int kind, const char *name)
+{
+    t_last_error = 0;
+    if (k != KERNEL_HIP) { fail(name, MFH_E_UNSUPPORTED); return; }
+    if (!Apl || !Bpl || !out || !p || RL < 1 || n < 1) { fail(name, MFH_E_ARG); return; }
+    pthread_mutex_lock(&g_lock);
+    mfh_ctx *c = NULL;
+    int rc = get_ctx(n, L, p, &c);
+    if (!rc) rc = mfh_mm(c, kind, Apl, Bpl, out, RL);
+    pthread_mutex_unlock(&g_lock);
+    if (rc) fail(name, rc);
+}
+
+void mm_mfft(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
+             const mfft_plan *p, kernel_t k, uint16_t *out, int RL)
+{
+    mm_common(Apl, Bpl, n, L, p, k, out, RL, MFH_IN_U16, "mm_mfft");
+}
+
+void mm_mfft_signed(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
+                    const mfft_plan *p, kernel_t k, uint16_t *out, int RL)
+{
+    mm_common(Apl, Bpl, n, L, p, k, out, RL, MFH_IN_U16_SIGNED, "mm_mfft_signed");
+}
+
+void conv_mfft(int64_t *Cw, const int32_t *A32, const int32_t *B32,
+               int n, int L, const mfft_plan *p, kernel_t k)
+{
+    t_last_error = 0;
+    if (k != KERNEL_HIP) { fail("conv_mfft", MFH_E_UNSUPPORTED); return; }
+    if (!Cw || !A32 || !B32 || !p || n < 1) { fail("conv_mfft", MFH_E_ARG); return; }
+    pthread_mutex_lock(&g_lock);
+    mfh_ctx *c = NULL;
+    int rc = get_ctx(n, L, p, &c);
+    if (!rc) rc = mfh_conv(c, A32, B32, Cw);
+    pthread_mutex_unlock(&g_lock);
+    if (rc) fail("conv_mfft", rc);
+}
+
+/* ---- fp32 embedding (src/fpfixed.c) -------------------------------------- */
+static int next_pow2(int x) { int r = 1; while (r < x) r <<= 1; return r; }
+
+/* exponent range of finite nonzero entries: x = mi 2^e2, mi in [2^23, 2^24)
+ * (src/fpfixed.c:40-54); host-side sizing, as in the reference */
+static void scan(const float *X, size_t nn, int *lo, int *hi, int *any)
+{
+    int l = 1 << 30, h = -(1 << 30), seen = 0;
+    for (size_t i = 0; i < nn; i++) {
+        float x = X[i];
+        if (x == 0.0f || !isfinite(x)) continue;
+        int e;
+        frexpf(x, &e);
+        if (e - 24 < l) l = e - 24;
+        if (e - 24 > h) h = e - 24;
+        seen = 1;
+    }
+    if (!seen) { l = 0; h = 0; }
+    *lo = l; *hi = h; *any = seen;
+}
+
+typedef struct { const float *A, *B; } fpx_src;
+
+int fpx_init(fpx_ctx *c, const float *A, const float *B, int n, int force_bits)
+{
+    size_t nn = (size_t)n * n;
+    int loA, hiA, loB, hiB, anyA, anyB;
+    scan(A, nn, &loA, &hiA, &anyA);
+    scan(B, nn, &loB, &hiB, &anyB);
+    memset(c, 0, sizeof *c);
+    c->sig = 24;
+    c->spreadA = anyA ? hiA - loA : 0;
+    c->spreadB = anyB ? hiB - loB : 0;
+    int L;
+    /* src/fpfixed.c:59-78 */
+    if (force_bits > 0) {
+        c->SA = c->SB = force_bits / 2;
+        L = next_pow2(force_bits / LIMB_BITS);
+    } else {
+        c->SA = -loA;
+        c->SB = -loB;
+        int spread = c->spreadA > c->spreadB ? c->spreadA : c->spreadB;
+        int bits = 24 + spread + 1;
+        int need = (bits + LIMB_BITS - 1) / LIMB_BITS;
+        int need2 = spread / LIMB_BITS + 3;
+        L = next_pow2(need > need2 ? need : need2);
+        if (L < 2) L = 2;
+    }
+    c->n = n; c->L = L;
+    /* src/fpfixed.c:84-88 */
+    if ((double)n * L * 65535.0 * 65535.0 > 4.0e18) {
+        fprintf(stderr, "fpx: n=%d L=%d would overflow int64 accumulators\n", n, L);
+        t_last_error = MFH_E_BOUND;
+        return -1;
+    }
+    c->A32 = calloc((size_t)L * nn, sizeof(int32_t));
+    c->B32 = calloc((size_t)L * nn, sizeof(int32_t));
+    c->Cw = calloc((size_t)(2 * L - 1) * nn, sizeof(int64_t));
+    if (!c->A32 || !c->B32 || !c->Cw) { fpx_free(c); return -1; }
+    return 0;
+}
+
+void fpx_encode(fpx_ctx *c, const float *A, const float *B)
+{
+    double t0 = now_sec();
+    t_last_error = 0;
+    int rc = mfh_fpx_encode(A, c->n, c->L, c->SA, c->A32);
+    if (!rc) rc = mfh_fpx_encode(B, c->n, c->L, c->SB, c->B32);
+    if (rc) { fail("fpx_encode", rc); return; }
+    fpx_src *s = c->dev ? (fpx_src *)c->dev : calloc(1, sizeof(fpx_src));
+    if (s) { s->A = A; s->B = B; c->dev = s; }
+    c->enc_secs = now_sec() - t0;
+}
+
+void fpx_decode_f32(fpx_ctx *c, float *C)
+{
+    double t0 = now_sec();
+    t_last_error = 0;
+    int rc = mfh_fpx_decode(c->Cw, c->n, c->L, c->SA + c->SB, C);
+    if (rc) { fail("fpx_decode_f32", rc); return; }
+    c->dec_secs = now_sec() - t0;
+}
+
+int fpx_mm_f32(fpx_ctx *c, const mfft_plan *p, float *C)
+{
+    t_last_error = 0;
+    fpx_src *s = (fpx_src *)c->dev;
+    if (!s || !p || !C) return fail("fpx_mm_f32", MFH_E_ARG);
+    pthread_mutex_lock(&g_lock);
+    mfh_ctx *h = NULL;
+    int rc = get_ctx(c->n, c->L, p, &h);
+    if (!rc) rc = mfh_fpx_mm(h, s->A, s->B, c->SA, c->SB, C);
+    pthread_mutex_unlock(&g_lock);
+    if (rc) return fail("fpx_mm_f32", rc);
+    return 0;
+}
+
+void fpx_free(fpx_ctx *c)
+{
+    free(c->A32); free(c->B32); free(c->Cw); free(c->dev);
+    c->A32 = NULL; c->B32 = NULL; c->Cw = NULL; c->dev = NULL;
+}

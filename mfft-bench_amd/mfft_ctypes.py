@@ -1,0 +1,239 @@
+"""ctypes binding of lib/libmfft_hip.so (include/mfftbench.h, include/mfft_hip.h).
+
+Plumbing for the tests and bench.py: every product call goes through the
+C-ABI into the gfx950 kernels.  Loading fails loudly when the library was not
+built; there is no fallback.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libmfft_hip.so")
+
+KERNEL_IKJ, KERNEL_PACKED, KERNEL_HIP = 0, 2, 12
+MFH_IN_U16, MFH_IN_U16_SIGNED, MFH_IN_I32 = 0, 1, 2
+ERRORS = {0: "MFH_OK", -1: "MFH_E_NODEV", -2: "MFH_E_NOMEM", -3: "MFH_E_ARG",
+          -4: "MFH_E_BOUND", -5: "MFH_E_RANGE", -6: "MFH_E_HIP", -7: "MFH_E_UNSUPPORTED"}
+
+
+class MfftError(RuntimeError):
+    def __init__(self, code, what=""):
+        self.code = code
+        super().__init__(f"{what}: {ERRORS.get(code, code)}")
+
+
+class Plan(C.Structure):
+    """mfft_plan / mfh_plan (identical layouts)."""
+    _fields_ = [("L", C.c_int), ("S", C.c_int), ("NB", C.c_int), ("K", C.c_int),
+                ("g", C.c_int), ("rec", C.c_int), ("nprod", C.c_longlong)]
+
+    def __repr__(self):
+        return f"Plan(L={self.L}, S={self.S}, NB={self.NB}, K={self.K}, g={self.g})"
+
+
+class FpxCtx(C.Structure):
+    _fields_ = [("n", C.c_int), ("L", C.c_int), ("sig", C.c_int),
+                ("SA", C.c_int), ("SB", C.c_int),
+                ("spreadA", C.c_int), ("spreadB", C.c_int),
+                ("A32", C.c_void_p), ("B32", C.c_void_p), ("Cw", C.c_void_p),
+                ("enc_secs", C.c_double), ("dec_secs", C.c_double),
+                ("dev", C.c_void_p)]
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+_lib = None
+
+
+def load(path=None):
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    path = path or LIB_PATH
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} not built: run `make -C mfft-bench_amd`")
+    L = C.CDLL(path)
+    vp, i, u64, sz = C.c_void_p, C.c_int, C.c_uint64, C.c_size_t
+    pl = C.POINTER(Plan)
+    sig = {
+        "mfh_strerror": ([i], C.c_char_p), "mfh_device_count": ([], i),
+        "mfh_device_arch": ([], C.c_char_p),
+        "mfh_create": ([C.POINTER(vp), i, i, pl], i), "mfh_destroy": ([vp], None),
+        "mfh_workspace_bytes": ([vp], sz),
+        "mfh_mm": ([vp, i, vp, vp, vp, i], i), "mfh_conv": ([vp, vp, vp, vp], i),
+        "mfh_mm_dev": ([vp, i, vp, vp, vp, i], i), "mfh_conv_dev": ([vp, vp, vp, vp], i),
+        "mfh_fpx_mm_dev": ([vp, vp, vp, i, i, vp], i), "mfh_fpx_mm": ([vp, vp, vp, i, i, vp], i),
+        "mfh_fpx_decode_dev": ([vp, vp, i, vp], i),
+        "mfh_normalize": ([vp, i, i, vp, i], i), "mfh_fpx_encode": ([vp, i, i, i, vp], i),
+        "mfh_fpx_decode": ([vp, i, i, i, vp], i),
+        "mfh_malloc": ([C.POINTER(vp), sz], i), "mfh_free": ([vp], i),
+        "mfh_h2d": ([vp, vp, sz], i), "mfh_d2h": ([vp, vp, sz], i), "mfh_sync": ([vp], i),
+        "mfh_rand_u16_dev": ([vp, vp, i, i, u64], i),
+        "mfh_rand_f32_dev": ([vp, vp, sz, u64, i, i], i),
+        "mfh_set_timing": ([vp, i], i), "mfh_stage_times": ([vp, C.POINTER(C.c_float)], i),
+        "mfh_work": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double)], i),
+        "mfft_plan_init": ([pl, i, i], i), "mfft_plan_products": ([pl], C.c_longlong),
+        "mfft_plan_maxbits": ([pl, i], C.c_double),
+        "mm_mfft": ([vp, vp, i, i, pl, i, vp, i], None),
+        "mm_mfft_signed": ([vp, vp, i, i, pl, i, vp, i], None),
+        "conv_mfft": ([vp, vp, vp, i, i, pl, i], None),
+        "normalize_planes": ([vp, i, i, vp, i], None),
+        "bigmat_rand": ([vp, i, i, u64], None),
+        "bigres_equal": ([vp, vp, i, i, vp, vp, vp], i),
+        "fpx_init": ([C.POINTER(FpxCtx), vp, vp, i, i], i),
+        "fpx_encode": ([C.POINTER(FpxCtx), vp, vp], None),
+        "fpx_decode_f32": ([C.POINTER(FpxCtx), vp], None),
+        "fpx_free": ([C.POINTER(FpxCtx)], None),
+        "fpx_mm_f32": ([C.POINTER(FpxCtx), pl, vp], i),
+        "mfft_last_error": ([], i), "mfft_strerror": ([i], C.c_char_p),
+        "kernel_name": ([i], C.c_char_p), "kernel_from_name": ([C.c_char_p], i),
+        "now_sec": ([], C.c_double),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    if path == LIB_PATH:
+        _lib = L
+    return L
+
+
+def check(rc, what=""):
+    if rc != 0:
+        raise MfftError(rc, what)
+
+
+def plan(L, sigma=0):
+    p = Plan()
+    if load().mfft_plan_init(C.byref(p), L, sigma) != 0:
+        return None
+    return p
+
+
+def have_gpu():
+    try:
+        lib = load()
+    except (OSError, FileNotFoundError):
+        return False
+    return lib.mfh_device_count() > 0 and lib.mfh_device_arch().startswith(b"gfx950")
+
+
+class Ctx:
+    """One device context (workspace for one n, L, plan)."""
+
+    def __init__(self, n, L, p=None):
+        self.lib = load()
+        self.n, self.L = n, L
+        self.plan = p or plan(L)
+        h = C.c_void_p()
+        check(self.lib.mfh_create(C.byref(h), n, L, C.byref(self.plan)), "mfh_create")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.mfh_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # host-buffer entry points
+    def mm(self, A, B, RL=None, signed=False):
+        RL = RL or 2 * self.L + 1
+        out = np.empty(RL * self.n * self.n, dtype=np.uint16)
+        kind = MFH_IN_U16_SIGNED if signed else MFH_IN_U16
+        check(self.lib.mfh_mm(self.h, kind, _p(A), _p(B), _p(out), RL), "mfh_mm")
+        return out
+
+    def conv(self, A32, B32):
+        cw = np.empty((2 * self.L - 1) * self.n * self.n, dtype=np.int64)
+        check(self.lib.mfh_conv(self.h, _p(A32), _p(B32), _p(cw)), "mfh_conv")
+        return cw
+
+    def fpx_mm(self, A, B, SA, SB):
+        out = np.empty(self.n * self.n, dtype=np.float32)
+        check(self.lib.mfh_fpx_mm(self.h, _p(A), _p(B), SA, SB, _p(out)), "mfh_fpx_mm")
+        return out
+
+    # device-level helpers
+    def set_timing(self, on=True):
+        check(self.lib.mfh_set_timing(self.h, int(on)))
+
+    def stage_times(self):
+        ms = (C.c_float * 5)()
+        check(self.lib.mfh_stage_times(self.h, ms), "mfh_stage_times")
+        return list(ms)
+
+    def work(self):
+        a, b, c = C.c_double(), C.c_double(), C.c_double()
+        check(self.lib.mfh_work(self.h, C.byref(a), C.byref(b), C.byref(c)))
+        return a.value, b.value, c.value
+
+    def sync(self):
+        check(self.lib.mfh_sync(self.h), "mfh_sync")
+
+
+class DevBuf:
+    def __init__(self, nbytes):
+        self.lib = load()
+        p = C.c_void_p()
+        check(self.lib.mfh_malloc(C.byref(p), nbytes), "mfh_malloc")
+        self.ptr, self.nbytes = p, nbytes
+
+    def upload(self, arr):
+        assert arr.nbytes <= self.nbytes
+        check(self.lib.mfh_h2d(self.ptr, _p(arr), arr.nbytes), "mfh_h2d")
+
+    def download(self, dtype, count):
+        out = np.empty(count, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        check(self.lib.mfh_d2h(_p(out), self.ptr, out.nbytes), "mfh_d2h")
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.lib.mfh_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+# ---- reference-named C API ---------------------------------------------------
+def mm_mfft(A, B, n, L, p, RL=None, kernel=KERNEL_HIP, signed=False):
+    lib = load()
+    RL = RL or 2 * L + 1
+    out = np.zeros(RL * n * n, dtype=np.uint16)
+    f = lib.mm_mfft_signed if signed else lib.mm_mfft
+    f(_p(A), _p(B), n, L, C.byref(p), kernel, _p(out), RL)
+    return out, lib.mfft_last_error()
+
+
+def conv_mfft(A32, B32, n, L, p, kernel=KERNEL_HIP):
+    lib = load()
+    cw = np.zeros((2 * L - 1) * n * n, dtype=np.int64)
+    lib.conv_mfft(_p(cw), _p(A32), _p(B32), n, L, C.byref(p), kernel)
+    return cw, lib.mfft_last_error()
+
+
+def normalize_planes(acc, nplanes, n, RL):
+    lib = load()
+    out = np.zeros(RL * n * n, dtype=np.uint16)
+    lib.normalize_planes(_p(np.ascontiguousarray(acc, np.int64)), nplanes, n, _p(out), RL)
+    return out, lib.mfft_last_error()
