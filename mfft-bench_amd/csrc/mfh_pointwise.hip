@@ -35,6 +35,8 @@
 //
 // Output C^[j][i][j'][t] int64: the K ring coefficients of one element are
 // contiguous, which is the order the inverse transform reads.
+#include <type_traits>
+
 #include "mfh_internal.hpp"
 
 namespace {
@@ -52,18 +54,39 @@ struct PwCfg {
     static constexpr int BI = 16 * WBI, BJ = 16 * WBJ;
     static constexpr int A_CHUNKS = K * WBI * 64;   // 16-byte LDS chunks
     static constexpr int B_CHUNKS = K * WBJ * 64;
-    static constexpr int LDS_BYTES = (A_CHUNKS + B_CHUNKS) * 16;
+    static constexpr int LDS_BYTES = 2 * (A_CHUNKS + B_CHUNKS) * 16;  // double-buffered
 };
 
 // One round: one 64-wide k block of one digit pair, all K values of c2.
 // la points at this wave's A fragment of ring coefficient 0 (stride
 // WBI*64 chunks per coefficient), lb likewise for B.
-template <class Cfg, bool ASC, int T0>
+template <class Cfg, bool ASC, int T0, class Issue>
 __device__ __forceinline__ void pw_round(v4i (&acc)[Cfg::T], const v4i *__restrict__ la,
-                                         const v4i *__restrict__ lb)
+                                         const v4i *__restrict__ lb, const Issue &issue)
 {
     constexpr int K = Cfg::K, T = Cfg::T;
     constexpr int SA = Cfg::WBI * 64, SB = Cfg::WBJ * 64;
+    if constexpr (T == K) {
+        // every A fragment is live at every step: hold all K of them
+        v4i af[K];
+#pragma unroll
+        for (int c1 = 0; c1 < K; ++c1) af[c1] = la[c1 * SA];
+#pragma unroll
+        for (int st = 0; st < K; ++st) {
+            const int c2 = ASC ? st : K - 1 - st;
+            const v4i bf = lb[c2 * SB];
+            issue(st);
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt) {
+                const int t = tt;
+                if ((ASC && c2 == t + 1) || (!ASC && c2 == t)) acc[tt] = -acc[tt];
+                acc[tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[pmod(t - c2, K)], bf,
+                                                                acc[tt], 0, 0, 0);
+            }
+        }
+        if (ASC) acc[K - 1] = -acc[K - 1];
+        return;
+    }
     v4i win[T + 1];
     constexpr int first = ASC ? 0 : K - 1;
     // window key kk = tt - c2 holds A fragment c1 = (T0 + kk) mod K in slot
@@ -78,6 +101,7 @@ __device__ __forceinline__ void pw_round(v4i (&acc)[Cfg::T], const v4i *__restri
     for (int st = 0; st < K; ++st) {
         const int c2 = ASC ? st : K - 1 - st;
         const v4i bf = lb[c2 * SB];
+        issue(st);
         if (st + 1 < K) {
             const int c2n = ASC ? st + 1 : K - 2 - st;
             const int ttn = ASC ? 0 : T - 1;
@@ -103,15 +127,65 @@ __device__ __forceinline__ void pw_round(v4i (&acc)[Cfg::T], const v4i *__restri
     }
 }
 
-template <class Cfg, bool ASC, int TG = 0>
+template <class Cfg, bool ASC, int TG = 0, class Issue>
 __device__ __forceinline__ void pw_dispatch(int tg, v4i (&acc)[Cfg::T], const v4i *la,
-                                            const v4i *lb)
+                                            const v4i *lb, const Issue &issue)
 {
     if constexpr (TG < Cfg::G) {
-        if (tg == TG) pw_round<Cfg, ASC, TG * Cfg::T>(acc, la, lb);
-        else pw_dispatch<Cfg, ASC, TG + 1>(tg, acc, la, lb);
+        if (tg == TG) pw_round<Cfg, ASC, TG * Cfg::T>(acc, la, lb, issue);
+        else pw_dispatch<Cfg, ASC, TG + 1>(tg, acc, la, lb, issue);
     }
 }
+
+// Round index -> (digit pair, k block).  Pairs are ordered by weight class
+// m = r + s so that each class's rounds are contiguous.
+__device__ __forceinline__ void pair_of(int p, int &r, int &s, int &m)
+{
+    // (r,s): (0,0) | (0,1) (1,0) | (0,2) (1,1) (2,0) | (1,2) (2,1) | (2,2),
+    // one nibble per pair index
+    constexpr unsigned long long R = 0x221210100ULL, S = 0x212012010ULL;
+    r = (int)((R >> (4 * p)) & 0xF);
+    s = (int)((S >> (4 * p)) & 0xF);
+    m = r + s;
+}
+
+// Direct-to-LDS loads of one round: for every ring coefficient, the
+// (16*WBI) x 64 A tile and the (16*WBJ) x 64 B^T tile, i.e. FA + FB
+// fragments of 16 x 64 bytes.  A fragment is one wave instruction: lane l
+// fetches row l%16, k bytes 16*(l/16)..+15, and global_load_lds_dwordx4
+// stores lane l's 16 bytes at fragment base + 16*l -- exactly the MFMA
+// operand order.  Wave w loads fragments w, w+WAVES, ...; the per-lane
+// offset is the same for all of them, so each load is a scalar base plus
+// one vector offset.  The loads of round r+1 are spread over the steps of
+// round r (one or more per step) so they never stall the MFMA stream.
+template <class Cfg>
+struct RoundLoads {
+    static constexpr int K = Cfg::K, WBI = Cfg::WBI, WBJ = Cfg::WBJ, W = Cfg::WAVES;
+    static constexpr int FA = K * WBI, FB = K * WBJ;
+    static constexpr int NA = FA / W, NB = FB / W;      // per wave
+    static_assert(FA % W == 0 && FB % W == 0, "fragments must split evenly over waves");
+    const int8_t *a0, *b0;      // this round's first A / B fragment of this wave
+    size_t da, db;              // byte step between a wave's consecutive fragments
+    v4i *lds_a, *lds_b;         // LDS destination of the first fragment
+    uint32_t lane_off;          // row * np + 16 * quarter
+    bool active;
+    __device__ __forceinline__ void operator()(int st) const
+    {
+        if (!active) return;
+        constexpr int N = NA + NB;
+        // loads i with i*K/N == st, i.e. i in [ceil(st*N/K), ceil((st+1)*N/K))
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            if ((i * K) / N != st) continue;
+            if (i < NA)
+                __builtin_amdgcn_global_load_lds((const void *)(a0 + i * da + lane_off),
+                                                 (void *)(lds_a + i * W * 64), 16, 0, 0);
+            else
+                __builtin_amdgcn_global_load_lds((const void *)(b0 + (i - NA) * db + lane_off),
+                                                 (void *)(lds_b + (i - NA) * W * 64), 16, 0, 0);
+        }
+    }
+};
 
 template <class Cfg>
 __global__ void __attribute__((amdgpu_flat_work_group_size(Cfg::THREADS, Cfg::THREADS),
@@ -120,8 +194,11 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
             int64_t *__restrict__ Ch, int np_, int tiles_j, int rounds_per_flush)
 {
     constexpr int K = Cfg::K, T = Cfg::T, WBI = Cfg::WBI, WBJ = Cfg::WBJ;
+    constexpr int BUF = Cfg::A_CHUNKS + Cfg::B_CHUNKS;   // 16-byte chunks per buffer
+    using RL_ = RoundLoads<Cfg>;
     extern __shared__ v4i lds[];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tg = wave / (WBI * WBJ);
     const int wb = wave % (WBI * WBJ);
     const int wbi = wb / WBJ, wbj = wb % WBJ;
@@ -131,8 +208,18 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     const size_t plane = (size_t)np_ * np_;
     const int8_t *Aj = Ah + (size_t)jp * K * MFH_DIGITS * plane;
     const int8_t *Bj = Bh + (size_t)jp * K * MFH_DIGITS * plane;
-    const v4i *la = lds + wbi * 64 + lane;
-    const v4i *lb = lds + Cfg::A_CHUNKS + wbj * 64 + lane;
+
+    // this wave's load slots: fragment f = wave + WAVES*i
+    //   A: f < FA, coefficient f / WBI, row block f % WBI
+    //   B: f - FA,  coefficient (f-FA) / WBJ, column block (f-FA) % WBJ
+    const int fa = wave, fb = wave;              // first slot of each kind
+    const int8_t *a_blk = Aj + (size_t)(fa / WBI) * MFH_DIGITS * plane +
+                          (size_t)(i0 + (fa % WBI) * 16) * np_;
+    const int8_t *b_blk = Bj + (size_t)(fb / WBJ) * MFH_DIGITS * plane +
+                          (size_t)(j0 + (fb % WBJ) * 16) * np_;
+    const size_t da = (size_t)(Cfg::WAVES / WBI) * MFH_DIGITS * plane;
+    const size_t db = (size_t)(Cfg::WAVES / WBJ) * MFH_DIGITS * plane;
+    const uint32_t lane_off = (uint32_t)((lane & 15) * np_ + (lane >> 4) * 16);
 
     long long tot[T][4];
     v4i acc[T];
@@ -144,54 +231,50 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     }
 
     const int kblocks = np_ / MFH_KBLK;
-    bool asc = true, last_asc = true;
+    const int rounds = MFH_DIGITS * MFH_DIGITS * kblocks;
+    auto loads_for = [&](int rd) {
+        RL_ q;
+        int r, s, m;
+        pair_of(rd / kblocks, r, s, m);
+        const int kb = rd % kblocks;
+        v4i *buf = lds + (rd & 1) * BUF;
+        q.a0 = a_blk + (size_t)r * plane + kb * MFH_KBLK;
+        q.b0 = b_blk + (size_t)s * plane + kb * MFH_KBLK;
+        q.da = da;
+        q.db = db;
+        q.lds_a = buf + fa * 64;
+        q.lds_b = buf + Cfg::A_CHUNKS + fb * 64;
+        q.lane_off = lane_off;
+        q.active = rd < rounds;
+        return q;
+    };
+    // prologue: round 0, all at once
+    {
+        RL_ q0 = loads_for(0);
+#pragma unroll
+        for (int st = 0; st < K; ++st) q0(st);
+    }
     int since = 0;
-    for (int m = 0; m < 2 * MFH_DIGITS - 1; ++m) {
-        const int rlo = m > MFH_DIGITS - 1 ? m - (MFH_DIGITS - 1) : 0;
-        const int rhi = m < MFH_DIGITS - 1 ? m : MFH_DIGITS - 1;
-        for (int r = rlo; r <= rhi; ++r) {
-            const int s = m - r;
-            const int8_t *Ar = Aj + (size_t)r * plane;
-            const int8_t *Bs = Bj + (size_t)s * plane;
-            for (int kb = 0; kb < kblocks; ++kb) {
-                __syncthreads();
-                // stage: 16-byte chunk (coefficient, 16-row block, row, k
-                // quarter); four consecutive threads read one 64-byte row
-                // segment, and the chunk lands at MFMA lane row + 16*quarter.
-                for (int q = tid; q < Cfg::A_CHUNKS; q += Cfg::THREADS) {
-                    const int c1 = q / (WBI * 64), rem = q % (WBI * 64);
-                    const int ib = rem >> 6, l2 = rem & 63, row = l2 >> 2, kq = l2 & 3;
-                    const int8_t *g = Ar + (size_t)c1 * MFH_DIGITS * plane +
-                                      (size_t)(i0 + ib * 16 + row) * np_ + kb * MFH_KBLK + kq * 16;
-                    lds[(c1 * WBI + ib) * 64 + row + 16 * kq] = *(const v4i *)g;
-                }
-                for (int q = tid; q < Cfg::B_CHUNKS; q += Cfg::THREADS) {
-                    const int c2 = q / (WBJ * 64), rem = q % (WBJ * 64);
-                    const int jb = rem >> 6, l2 = rem & 63, row = l2 >> 2, kq = l2 & 3;
-                    const int8_t *g = Bs + (size_t)c2 * MFH_DIGITS * plane +
-                                      (size_t)(j0 + jb * 16 + row) * np_ + kb * MFH_KBLK + kq * 16;
-                    lds[Cfg::A_CHUNKS + (c2 * WBJ + jb) * 64 + row + 16 * kq] = *(const v4i *)g;
-                }
-                __syncthreads();
-                if (asc) pw_dispatch<Cfg, true>(tg, acc, la, lb);
-                else     pw_dispatch<Cfg, false>(tg, acc, la, lb);
-                last_asc = asc;
-                asc = !asc;
-                if (++since == rounds_per_flush) {
-                    // after an ascending round acc = -(P-N), else +(P-N)
-                    const long long w = (last_asc ? -1LL : 1LL) << (8 * m);
-#pragma unroll
-                    for (int tt = 0; tt < T; ++tt) {
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) tot[tt][v] += (long long)acc[tt][v] * w;
-                        acc[tt] = v4i{0, 0, 0, 0};
-                    }
-                    since = 0;
-                }
-            }
-        }
-        if (since) {
-            const long long w = (last_asc ? -1LL : 1LL) << (8 * m);
+    auto one_round = [&](int rd, auto asc_tag) {
+        constexpr bool ASC = decltype(asc_tag)::value;
+        const v4i *cur = lds + (rd & 1) * BUF;
+        // this round's tiles have landed (own loads), and every wave is done
+        // with the buffer the next round's loads overwrite
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const RL_ q = loads_for(rd + 1);
+        const v4i *la = cur + wbi * 64 + lane;
+        const v4i *lb = cur + Cfg::A_CHUNKS + wbj * 64 + lane;
+        pw_dispatch<Cfg, ASC>(tg, acc, la, lb, q);
+        ++since;
+        int r, s, m, rn, sn, mn;
+        pair_of(rd / kblocks, r, s, m);
+        const bool last = rd + 1 == rounds;
+        mn = m;
+        if (!last) pair_of((rd + 1) / kblocks, rn, sn, mn);
+        if (last || mn != m || since == rounds_per_flush) {
+            // after an ascending round acc = -(P-N), after a descending one +(P-N)
+            const long long w = (ASC ? -1LL : 1LL) << (8 * m);
 #pragma unroll
             for (int tt = 0; tt < T; ++tt) {
 #pragma unroll
@@ -200,7 +283,13 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
             }
             since = 0;
         }
+    };
+    int rd = 0;
+    for (; rd + 1 < rounds; rd += 2) {
+        one_round(rd, std::true_type{});
+        one_round(rd + 1, std::false_type{});
     }
+    if (rd < rounds) one_round(rd, std::true_type{});
 
     // epilogue: lane holds rows 4*(lane/16)+v, column lane%16 of its block
     const int col = j0 + wbj * 16 + (lane & 15);
@@ -241,7 +330,7 @@ int mfh_launch_pointwise(mfh_ctx *c)
     case 4:  return launch_cfg<PwCfg<4, 4, 2, 2>>(c);
     case 8:  return launch_cfg<PwCfg<8, 8, 2, 2>>(c);
     case 16: return launch_cfg<PwCfg<16, 16, 2, 2>>(c);
-    case 32: return launch_cfg<PwCfg<32, 16, 1, 2>>(c);
+    case 32: return launch_cfg<PwCfg<32, 8, 1, 1>>(c);
     default: return MFH_E_UNSUPPORTED;
     }
 }
