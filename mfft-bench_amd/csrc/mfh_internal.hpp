@@ -41,6 +41,7 @@ struct mfh_ctx {
     int n, np;            // matrix size, padded to a multiple of 64
     int L, S, NB, K, g;
     int dev;
+    int use_fast;         // compile-time specialised kernels when available
     hipStream_t stream;
     // workspace
     int8_t *dAh, *dBh;    // digit planes [NB][K][3][np][np]

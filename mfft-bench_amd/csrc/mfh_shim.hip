@@ -1,7 +1,8 @@
 // mfh_shim.hip -- extern "C" entry points of mfft_hip.h: device contexts,
 // workspace, the product pipelines and timing.
-#include <string.h>
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include "mfh_internal.hpp"
 
@@ -147,6 +148,7 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     memset(c, 0, sizeof *c);
     c->n = n; c->np = np_; c->L = L; c->S = p->S; c->NB = p->NB; c->K = p->K; c->g = p->g;
     c->dev = 0;
+    c->use_fast = getenv("MFH_GENERIC_KERNELS") ? 0 : 1;
     if (hipSetDevice(0) != hipSuccess || hipStreamCreate(&c->stream) != hipSuccess) {
         delete c;
         return MFH_E_HIP;

@@ -9,6 +9,9 @@
 //     X[j] = sum_b omega^(j*b) x_b,   j = 0 .. NB-1   (natural order).
 // Multiplying by y^e is a negacyclic shift, so every output coefficient is
 // a signed sum of input limbs: no multiplications anywhere.
+#include <type_traits>
+#include <utility>
+
 #include "mfh_internal.hpp"
 
 namespace {
@@ -115,6 +118,198 @@ __global__ __launch_bounds__(256) void k_forward_generic(
             o[2 * nnp] = (int8_t)d2;
         }
     }
+}
+
+// ---- forward transform, plan specialised at compile time ----------------------
+// One thread per element; the element's L limbs are held in registers (u16
+// pairs packed in one VGPR).  The NB output points are split into Q residue
+// classes j = q + Q*j' (j' < P = NB/Q):
+//     X[q + Q j'] = sum_{b' < P} w^(j' b') z_q[b'],   w = omega^Q,
+//     z_q[b']     = sum_{b = b' mod P} omega^(q b) x_b
+// (the twist omega^(q b) = y^(g q b) is a negacyclic shift, the fold adds
+// the L/S non-zero blocks into P), and each class is a length-P radix-2
+// DIF transform over K-vectors.  Every shift is a compile-time register
+// renaming; only additions and negations remain.
+template <int L>
+struct LimbsPacked {           // unsigned limbs, two per VGPR
+    uint32_t r[L / 2];
+    bool top_signed;
+    __device__ __forceinline__ int get(int u) const
+    {
+        const uint32_t w = r[u / 2];
+        if (u == L - 1 && top_signed) return (int)(short)(w >> 16);
+        return (u & 1) ? (int)(w >> 16) : (int)(w & 0xFFFFu);
+    }
+};
+template <int L>
+struct LimbsI32 {
+    int r[L];
+    __device__ __forceinline__ int get(int u) const { return r[u]; }
+};
+
+// Packed limb pairs staged in LDS for the whole workgroup: pair p of
+// element slot t at lds[p * 256 + t] (consecutive threads read consecutive
+// dwords: conflict-free).  Filled with 16-byte loads of 8 consecutive
+// elements of planes 2p and 2p+1 (the input row length must be a multiple
+// of 8, so such a run never straddles a row end).
+template <int L>
+struct LimbsLds {
+    const uint32_t *base;      // lds + thread slot
+    bool top_signed;
+    __device__ __forceinline__ int get(int u) const
+    {
+        const uint32_t w = base[(u / 2) * 256];
+        if (u == L - 1 && top_signed) return (int)(short)(w >> 16);
+        return (u & 1) ? (int)(w >> 16) : (int)(w & 0xFFFFu);
+    }
+};
+
+template <int L>
+__device__ __forceinline__ void stage_limbs_u16(uint32_t *lds, const uint16_t *src, int n,
+                                                size_t nn, int np_, size_t e0)
+{
+    constexpr int NP2 = L / 2;
+    for (int t = threadIdx.x; t < NP2 * 32; t += 256) {
+        const int p = t >> 5, g8 = t & 31;
+        const size_t e = e0 + 8 * g8;
+        const int i = (int)(e / np_), k = (int)(e % np_);
+        uint4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+        if (i < n && k < n) {
+            lo = *(const uint4 *)(src + (size_t)(2 * p) * nn + (size_t)i * n + k);
+            hi = *(const uint4 *)(src + (size_t)(2 * p + 1) * nn + (size_t)i * n + k);
+        }
+        uint32_t w[8];
+        const uint32_t l4[4] = {lo.x, lo.y, lo.z, lo.w}, h4[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            w[2 * d] = __builtin_amdgcn_perm(h4[d], l4[d], 0x05040100u);     // lo16(l)|lo16(h)<<16
+            w[2 * d + 1] = __builtin_amdgcn_perm(h4[d], l4[d], 0x07060302u); // hi16(l)|hi16(h)<<16
+        }
+        uint4 *dst = (uint4 *)(lds + p * 256 + 8 * g8);
+        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
+}
+
+template <int L, class Src>
+__device__ __forceinline__ void load_limbs(LimbsPacked<L> &x, const Src &src, int i, int k,
+                                           bool valid)
+{
+#pragma unroll
+    for (int u = 0; u < L; u += 2) {
+        uint32_t lo = valid ? (uint32_t)(uint16_t)src.get(u, i, k) : 0u;
+        uint32_t hi = valid ? (uint32_t)(uint16_t)src.get(u + 1, i, k) : 0u;
+        x.r[u / 2] = lo | (hi << 16);
+    }
+}
+template <int L, class Src>
+__device__ __forceinline__ void load_limbs(LimbsI32<L> &x, const Src &src, int i, int k,
+                                           bool valid)
+{
+#pragma unroll
+    for (int u = 0; u < L; ++u) x.r[u] = valid ? src.get(u, i, k) : 0;
+}
+
+// balanced base-2^8 digits of v: bytes of v, (v + 2^7) >> 8, (v + 2^15 + 2^7) >> 16
+__device__ __forceinline__ void store_digits(int8_t *p, size_t nnp, int v)
+{
+    p[0] = (int8_t)v;
+    p[nnp] = (int8_t)((v + 128) >> 8);
+    p[2 * nnp] = (int8_t)((v + 32896) >> 16);
+}
+
+// One output class q (compile time): twist + fold, length-P DIF, digits.
+template <int S, int NB, int Q, int q, class Limbs>
+__device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t nnp)
+{
+    constexpr int K = 2 * S, P = NB / Q, LS = NB / 2;
+    constexpr int g = 2 * K / NB, twoK = 2 * K;
+    int z[P][K];
+#pragma unroll
+    for (int bp = 0; bp < P; ++bp)
+#pragma unroll
+        for (int c = 0; c < K; ++c) z[bp][c] = 0;
+    // twist by omega^(q b) = y^(g q b) and fold the non-zero blocks
+    // (ring coefficients c < S) of residue b mod P
+#pragma unroll
+    for (int b = 0; b < LS; ++b) {
+#pragma unroll
+        for (int c = 0; c < S; ++c) {
+            const int pos = (c + (g * q * b) % twoK) % twoK;
+            const int v = x.get(b * S + c);
+            if (pos < K) z[b % P][pos] += v;
+            else         z[b % P][pos - K] -= v;
+        }
+    }
+    // length-P DIF with root w = y^(g Q): natural in, bit-reversed out;
+    // butterfly u' = u + v, v' = (u - v) y^e
+#pragma unroll
+    for (int len = P; len >= 2; len >>= 1) {
+#pragma unroll
+        for (int j0 = 0; j0 < P; j0 += len) {
+#pragma unroll
+            for (int t = 0; t < len / 2; ++t) {
+                const int ex = (g * Q * t * (P / len)) % twoK;
+                int d[K];
+#pragma unroll
+                for (int c = 0; c < K; ++c) {
+                    const int a = z[j0 + t][c], bb = z[j0 + t + len / 2][c];
+                    z[j0 + t][c] = a + bb;
+                    d[c] = a - bb;
+                }
+#pragma unroll
+                for (int c = 0; c < K; ++c) {
+                    const int pos = (c + ex) % twoK;
+                    if (pos < K) z[j0 + t + len / 2][pos] = d[c];
+                    else         z[j0 + t + len / 2][pos - K] = -d[c];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int pos = 0; pos < P; ++pos) {
+        int jp = 0;
+#pragma unroll
+        for (int bit = 1, rb = P >> 1; bit < P; bit <<= 1, rb >>= 1)
+            if (pos & bit) jp |= rb;
+        const int j = q + Q * jp;
+#pragma unroll
+        for (int c = 0; c < K; ++c)
+            store_digits(o + (size_t)((j * K + c) * MFH_DIGITS) * nnp, nnp, z[pos][c]);
+    }
+}
+
+template <int S, int NB, int Q, class Limbs, int... qs>
+__device__ __forceinline__ void forward_classes(const Limbs &x, int8_t *o, size_t nnp,
+                                                std::integer_sequence<int, qs...>)
+{
+    (forward_class<S, NB, Q, qs, Limbs>(x, o, nnp), ...);
+}
+
+template <int S, int NB, int Q, class Limbs, class Src>
+__global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restrict__ out, int np_,
+                                                      int top_signed)
+{
+    constexpr int L = NB * S / 2;
+    const size_t nnp = (size_t)np_ * np_;
+    const size_t e0 = (size_t)blockIdx.x * 256;
+    const size_t e = e0 + threadIdx.x;
+    Limbs x;
+    if constexpr (std::is_same_v<Limbs, LimbsLds<L>>) {
+        __shared__ uint32_t stage[(L / 2) * 256];
+        stage_limbs_u16<L>(stage, src.p, src.n, src.nn, np_, e0);
+        __syncthreads();
+        x.base = stage + threadIdx.x;
+        x.top_signed = top_signed != 0;
+        if (e >= nnp) return;
+    } else {
+        if (e >= nnp) return;
+        const int i = (int)(e / np_), k = (int)(e % np_);
+        const bool valid = i < src.n && k < src.n;
+        load_limbs<L>(x, src, i, k, valid);
+        if constexpr (std::is_same_v<Limbs, LimbsPacked<L>>) x.top_signed = top_signed != 0;
+    }
+    forward_classes<S, NB, Q, Limbs>(x, out + e, nnp, std::make_integer_sequence<int, Q>{});
 }
 
 // |limb| <= 65535 for int32 inputs (the transform and digit bounds assume it)
@@ -380,6 +575,28 @@ int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
     return MFH_OK;
 }
 
+namespace {
+// compile-time plans: (S, NB) with the class count Q = NB/4
+template <int S, int NB, class Src, class Limbs>
+bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_signed)
+{
+    if (c->S != S || c->NB != NB) return false;
+    const size_t nnp = (size_t)c->np * c->np;
+    hipLaunchKernelGGL((k_forward_fast<S, NB, NB / 4, Limbs, Src>),
+                       dim3((unsigned)((nnp + 255) / 256)), dim3(256), 0, c->stream, s, dst,
+                       c->np, top_signed);
+    return true;
+}
+
+bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int top_signed)
+{
+    if (c->n % 8) return false;   // staged 16-byte loads need rows of 8k limbs
+    return try_fast<8, 32, SrcU16, LimbsLds<128>>(c, s, dst, top_signed) ||   // W=2048
+           try_fast<8, 16, SrcU16, LimbsLds<64>>(c, s, dst, top_signed) ||    // W=1024
+           try_fast<4, 16, SrcU16, LimbsPacked<32>>(c, s, dst, top_signed);   // W=512
+}
+}  // namespace
+
 int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
                        int scale_S)
 {
@@ -387,6 +604,20 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
     const size_t nn = (size_t)c->n * c->n;
     dim3 grid((unsigned)((nnp + 255) / 256));
     const int LS = c->L / c->S;
+    if (c->use_fast) {
+        bool done = false;
+        if (in_kind == MFH_IN_U16 || in_kind == MFH_IN_U16_SIGNED) {
+            SrcU16 s{(const uint16_t *)src, nn, c->n, c->L};
+            done = forward_fast_u16(c, s, dst, in_kind == MFH_IN_U16_SIGNED);
+        } else if (in_kind == MFH_IN_F32) {
+            SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
+            done = try_fast<4, 16, SrcF32, LimbsI32<32>>(c, s, dst, 0);       // 512-bit grid
+        }
+        if (done) {
+            MFH_HIP(hipGetLastError());
+            return MFH_OK;
+        }
+    }
     switch (in_kind) {
     case MFH_IN_U16: {
         SrcU16 s{(const uint16_t *)src, nn, c->n, c->L};
