@@ -385,6 +385,90 @@ __global__ void k_inverse_fold(const int64_t *__restrict__ Ch,
     }
 }
 
+// ---- inverse transform + /NB + fold, plan specialised ------------------------
+// K lanes per element (lane c = ring coefficient c); each lane holds the NB
+// values C^[j][c] of its element in registers, loaded in bit-reversed point
+// order, and runs the Cooley-Tukey stages (conjugate twiddles) fully
+// unrolled.  Multiplying the ring element in lanes c = 0..K-1 by y^-e is a
+// lane rotation (ds_bpermute) plus a sign per lane:
+//     (y^-e v)[c] = +-v[(c + e) mod K],  minus iff floor((c + e)/K) is odd.
+// Fold: Cw[b*S + c] = x_b[c]/NB + x_(b-1)[c+S]/NB for the lanes c < S (the
+// second term is one more rotation).  Cw goes through LDS so that each plane
+// is written as one contiguous run of the workgroup's elements.
+__device__ __forceinline__ long long bperm64(long long v, int addr)
+{
+    const int lo = __builtin_amdgcn_ds_bpermute(addr, (int)(unsigned long long)v);
+    const int hi = __builtin_amdgcn_ds_bpermute(addr, (int)((unsigned long long)v >> 32));
+    return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+
+template <int NB, int K>
+__global__ __launch_bounds__(256) void k_inverse_fast(const int64_t *__restrict__ Ch,
+                                                      int64_t *__restrict__ Cw, int n, int np_,
+                                                      int P)
+{
+    constexpr int S = K / 2, g = 2 * K / NB, twoK = 2 * K;
+    constexpr int PASS = 256 / K;            // elements per pass
+    constexpr int E = 2 * PASS;              // elements per workgroup
+    constexpr int LG = __builtin_ctz(NB);
+    extern __shared__ int64_t cwl[];         // [P][E]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int c = lane % K;
+    const int gbase = (lane / K) * K;        // first lane of this element's group
+    const size_t nn = (size_t)n * n;
+    const size_t e0 = (size_t)blockIdx.x * E;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        const int el = pass * PASS + tid / K;
+        const size_t e = e0 + el;
+        const bool valid = e < nn;
+        const int i = valid ? (int)(e / n) : 0, jj = valid ? (int)(e % n) : 0;
+        long long X[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            int r = 0;
+#pragma unroll
+            for (int bit = 1, rb = NB >> 1; bit < NB; bit <<= 1, rb >>= 1)
+                if (j & bit) r |= rb;
+            X[r] = valid ? Ch[(((size_t)j * np_ + i) * np_ + jj) * K + c] : 0;
+        }
+#pragma unroll
+        for (int len = 2; len <= NB; len <<= 1) {
+#pragma unroll
+            for (int j0 = 0; j0 < NB; j0 += len) {
+#pragma unroll
+                for (int t = 0; t < len / 2; ++t) {
+                    const int ex = (g * t * (NB / len)) % twoK;
+                    const int p = j0 + t, q = p + len / 2;
+                    long long w = X[q];
+                    if (ex != 0) {
+                        const int raw = c + ex;                   // < 3K
+                        w = bperm64(w, (gbase + raw % K) * 4);
+                        if ((raw / K) & 1) w = -w;
+                    }
+                    const long long u = X[p];
+                    X[p] = u + w;
+                    X[q] = u - w;
+                }
+            }
+        }
+        // fold and /NB (every value is an exact multiple of NB)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            long long hiw = 0;
+            if (b > 0) hiw = bperm64(X[b - 1], (gbase + (c + S) % K) * 4) >> LG;
+            const int w = b * S + c;
+            if (c < S && w < P) cwl[(size_t)w * E + el] = (X[b] >> LG) + hiw;
+        }
+    }
+    __syncthreads();
+    const int ecount = (int)((nn - e0) < (size_t)E ? (nn - e0) : (size_t)E);
+    for (int idx = tid; idx < P * E; idx += 256) {
+        const int w = idx / E, el = idx % E;
+        if (el < ecount) Cw[(size_t)w * nn + e0 + el] = cwl[idx];
+    }
+}
+
 // ---- carry normalisation (src/bigmat.c:48-60) ------------------------------
 __global__ __launch_bounds__(256) void k_carry(const int64_t *__restrict__ Cw,
                                                uint16_t *__restrict__ out,
@@ -659,8 +743,38 @@ int mfh_launch_check_i32(mfh_ctx *c, const int32_t *src, int planes)
     return MFH_OK;
 }
 
+namespace {
+template <int NB, int K>
+bool try_inverse_fast(mfh_ctx *c, int64_t *Cw)
+{
+    if (c->NB != NB || c->K != K) return false;
+    constexpr int E = 2 * (256 / K);
+    const int P = 2 * c->L - 1;
+    const size_t lds = (size_t)P * E * sizeof(int64_t);
+    if (lds > 160 * 1024) return false;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void *)k_inverse_fast<NB, K>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                160 * 1024) != hipSuccess)
+            return false;
+        attr_set = true;
+    }
+    const size_t nn = (size_t)c->n * c->n;
+    hipLaunchKernelGGL((k_inverse_fast<NB, K>), dim3((unsigned)((nn + E - 1) / E)), dim3(256),
+                       lds, c->stream, c->dCh, Cw, c->n, c->np, P);
+    return true;
+}
+}  // namespace
+
 int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw)
 {
+    if (c->use_fast && (try_inverse_fast<32, 16>(c, Cw) ||   // W=2048
+                        try_inverse_fast<16, 16>(c, Cw) ||   // W=1024
+                        try_inverse_fast<16, 8>(c, Cw))) {   // W=512
+        MFH_HIP(hipGetLastError());
+        return MFH_OK;
+    }
     const int blk = c->NB * c->K;
     int epw = 8192 / blk;              // 2 * epw * blk * 8 bytes <= 128 KiB
     if (epw > 64) epw = 64;
