@@ -20,21 +20,46 @@
 //
 // Pointwise accumulators: one MFMA term is |d_A * d_B| <= 2^14.  A round
 // (one 64-wide k block of one digit pair, all K ring coefficients) adds
-// K*64 terms to an int32 accumulator, i.e. at most K * 2^20 in magnitude, so
-// the int32 accumulators are flushed into int64 totals after at most
-// floor((2^31 - 1) / (K * 2^20)) rounds.
+// K*64 terms to an int32 accumulator, i.e. at most K * 2^20 in magnitude.
+// A digit-weight class m = r+s has at most 3 digit pairs, so its int32
+// result is bounded by 3 * (np/64) * K * 2^20, which must stay below 2^31.
+// The pointwise step writes the five class results; the inverse transform
+// recombines C^ = sum_m class_m * 2^(8m) in int64.
 //
-// int64 totals: |C^| <= K * n * ((NB/2) * 65535)^2, and the inverse
-// transform multiplies by at most NB more; both must stay below 2^62.
+// int64: |C^| <= K * n * ((NB/2) * 65535)^2, and the inverse transform
+// multiplies by at most NB more; both must stay below 2^62.
 // ---------------------------------------------------------------------------
 #define MFH_DIGITS 3
 #define MFH_DIGIT_MAX 8355711LL   // 127 * (1 + 2^8 + 2^16)
 #define MFH_DIGIT_MIN (-8421504LL) // -128 * (1 + 2^8 + 2^16)
 #define MFH_KBLK 64               // k extent of one MFMA operand block
 
-static inline int mfh_rounds_per_flush(int K)
+// Digit modes of the transformed values.
+//  MFH_MODE_B8: three balanced base-2^8 digits d0, d1, d2 in [-128, 127];
+//    9 digit products, accumulated in 5 weight classes m = r+s (2^(8m)).
+//  MFH_MODE_K7: three balanced base-2^7 digits d0, d1, d2 in [-64, 63] plus
+//    the pairwise sums d0+d1, d0+d2, d1+d2 (in [-128, 126], still int8):
+//    Karatsuba's 6 products P0 = a0 b0, P1 = a1 b1, P2 = a2 b2,
+//    P3 = (a0+a1)(b0+b1), P4 = (a0+a2)(b0+b2), P5 = (a1+a2)(b1+b2), one
+//    class each, recombined as
+//      c0 = P0, c1 = P3-P0-P1, c2 = P4-P0-P2+P1, c3 = P5-P1-P2, c4 = P2,
+//      C^ = sum_m c_m 2^(7m).
+//    Range: [-64 (1+2^7+2^14), 63 (1+2^7+2^14)] = [-1056832, 1040319].
+#define MFH_MODE_B8 0
+#define MFH_MODE_K7 1
+#define MFH_K7_MAX 1040319LL
+#define MFH_PLANES_MAX 6          // digit planes per (point, coefficient)
+#define MFH_CLASSES_MAX 6         // int32 class results per (point, element, t)
+static inline int mfh_planes(int mode) { return mode == MFH_MODE_K7 ? 6 : 3; }
+static inline int mfh_nclasses(int mode) { return mode == MFH_MODE_K7 ? 6 : 5; }
+
+#define MFH_CLASSES (2 * MFH_DIGITS - 1)
+
+// class accumulators provably fit int32: a class has at most 3 (B8) or 1
+// (K7) digit products of np/64 rounds, each round at most K * 64 * 2^14
+static inline bool mfh_class_bound_ok(int K, int np_)
 {
-    return (int)((2147483647LL) / ((long long)K << 20));
+    return 3LL * (np_ / MFH_KBLK) * ((long long)K << 20) <= 2147483647LL;
 }
 
 struct mfh_ctx {
@@ -44,8 +69,11 @@ struct mfh_ctx {
     int use_fast;         // compile-time specialised kernels when available
     hipStream_t stream;
     // workspace
-    int8_t *dAh, *dBh;    // digit planes [NB][K][3][np][np]
-    int64_t *dCh;         // pointwise products [NB][np][np][K]
+    int mode;             // digit mode of the current product (MFH_MODE_*)
+    int recode;           // forward transform recodes limbs to signed form
+    int k7_ok;            // plan admits MFH_MODE_K7 (workspace sized for it)
+    int8_t *dAh, *dBh;    // digit planes [NB][K][planes][np][np]
+    int32_t *dC5;         // pointwise class results [NB][np][np][classes][K]
     int64_t *dCw;         // coefficient planes [2L-1][n][n]
     void *dBt;            // transposed B input, up to L*n*n int32
     int *dFlag;           // device error flags

@@ -54,7 +54,7 @@ struct PwCfg {
     static constexpr int BI = 16 * WBI, BJ = 16 * WBJ;
     static constexpr int A_CHUNKS = K * WBI * 64;   // 16-byte LDS chunks
     static constexpr int B_CHUNKS = K * WBJ * 64;
-    static constexpr int LDS_BYTES = 2 * (A_CHUNKS + B_CHUNKS) * 16;  // double-buffered
+    static constexpr int LDS_BYTES = (A_CHUNKS + B_CHUNKS) * 16;   // one round buffer
 };
 
 // One round: one 64-wide k block of one digit pair, all K values of c2.
@@ -67,22 +67,37 @@ __device__ __forceinline__ void pw_round(v4i (&acc)[Cfg::T], const v4i *__restri
     constexpr int K = Cfg::K, T = Cfg::T;
     constexpr int SA = Cfg::WBI * 64, SB = Cfg::WBJ * 64;
     if constexpr (T == K) {
-        // every A fragment is live at every step: hold all K of them
+        // every A fragment is live at every step: hold all K of them.
+        // Step st uses B fragment c2 (ascending or descending).  The
+        // accumulator whose sign flips at the start of the next step is
+        // issued first in this step (the flip then waits on nothing), B
+        // fragments are read two steps ahead, and scheduling barriers keep
+        // the compiler from hoisting a flip next to its producing MFMA.
         v4i af[K];
 #pragma unroll
         for (int c1 = 0; c1 < K; ++c1) af[c1] = la[c1 * SA];
+        v4i bq[3];
+        bq[0] = lb[(ASC ? 0 : K - 1) * SB];
+        if (K > 1) bq[1] = lb[(ASC ? 1 : K - 2) * SB];
 #pragma unroll
         for (int st = 0; st < K; ++st) {
             const int c2 = ASC ? st : K - 1 - st;
-            const v4i bf = lb[c2 * SB];
-            issue(st);
+            if (st + 2 < K) bq[(st + 2) % 3] = lb[(ASC ? st + 2 : K - 3 - st) * SB];
+            // flips at this step: ASC flips t = c2-1 (after its last positive
+            // term), DESC flips t = c2 (before its first positive term)
+            if (ASC && c2 >= 1) acc[c2 - 1] = -acc[c2 - 1];
+            if (!ASC) acc[c2] = -acc[c2];
+            // first the accumulator flipped at the next step: ASC t = c2,
+            // DESC t = c2-1; then the rest in cyclic order
+            const int lead = ASC ? c2 : (c2 + K - 1) % K;
 #pragma unroll
-            for (int tt = 0; tt < T; ++tt) {
-                const int t = tt;
-                if ((ASC && c2 == t + 1) || (!ASC && c2 == t)) acc[tt] = -acc[tt];
-                acc[tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[pmod(t - c2, K)], bf,
-                                                                acc[tt], 0, 0, 0);
+            for (int o = 0; o < T; ++o) {
+                const int t = (lead + o) % K;
+                acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[pmod(t - c2, K)], bq[st % 3],
+                                                               acc[t], 0, 0, 0);
             }
+            issue(st);
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (ASC) acc[K - 1] = -acc[K - 1];
         return;
@@ -156,46 +171,74 @@ __device__ __forceinline__ void pair_of(int p, int &r, int &s, int &m)
 // stores lane l's 16 bytes at fragment base + 16*l -- exactly the MFMA
 // operand order.  Wave w loads fragments w, w+WAVES, ...; the per-lane
 // offset is the same for all of them, so each load is a scalar base plus
-// one vector offset.  The loads of round r+1 are spread over the steps of
-// round r (one or more per step) so they never stall the MFMA stream.
+// one vector offset.
 template <class Cfg>
-struct RoundLoads {
-    static constexpr int K = Cfg::K, WBI = Cfg::WBI, WBJ = Cfg::WBJ, W = Cfg::WAVES;
-    static constexpr int FA = K * WBI, FB = K * WBJ;
-    static constexpr int NA = FA / W, NB = FB / W;      // per wave
-    static_assert(FA % W == 0 && FB % W == 0, "fragments must split evenly over waves");
-    const int8_t *a0, *b0;      // this round's first A / B fragment of this wave
-    size_t da, db;              // byte step between a wave's consecutive fragments
-    v4i *lds_a, *lds_b;         // LDS destination of the first fragment
-    uint32_t lane_off;          // row * np + 16 * quarter
-    bool active;
-    __device__ __forceinline__ void operator()(int st) const
-    {
-        if (!active) return;
-        constexpr int N = NA + NB;
-        // loads i with i*K/N == st, i.e. i in [ceil(st*N/K), ceil((st+1)*N/K))
+__device__ __forceinline__ void pw_load_round(v4i *buf, const int8_t *a0, const int8_t *b0,
+                                              size_t da, size_t db, int fa, int fb,
+                                              uint32_t lane_off)
+{
+    constexpr int W = Cfg::WAVES;
+    constexpr int NA = Cfg::K * Cfg::WBI / W, NB = Cfg::K * Cfg::WBJ / W;
+    static_assert((Cfg::K * Cfg::WBI) % W == 0 && (Cfg::K * Cfg::WBJ) % W == 0,
+                  "fragments must split evenly over waves");
 #pragma unroll
-        for (int i = 0; i < N; ++i) {
-            if ((i * K) / N != st) continue;
-            if (i < NA)
-                __builtin_amdgcn_global_load_lds((const void *)(a0 + i * da + lane_off),
-                                                 (void *)(lds_a + i * W * 64), 16, 0, 0);
-            else
-                __builtin_amdgcn_global_load_lds((const void *)(b0 + (i - NA) * db + lane_off),
-                                                 (void *)(lds_b + (i - NA) * W * 64), 16, 0, 0);
-        }
-    }
+    for (int i = 0; i < NA; ++i)
+        __builtin_amdgcn_global_load_lds((const void *)(a0 + i * da + lane_off),
+                                         (void *)(buf + (fa + i * W) * 64), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+        __builtin_amdgcn_global_load_lds((const void *)(b0 + i * db + lane_off),
+                                         (void *)(buf + Cfg::A_CHUNKS + (fb + i * W) * 64), 16,
+                                         0, 0);
+}
+
+struct NoIssue {
+    __device__ __forceinline__ void operator()(int) const {}
 };
 
-template <class Cfg>
-__global__ void __attribute__((amdgpu_flat_work_group_size(Cfg::THREADS, Cfg::THREADS),
-                               amdgpu_waves_per_eu(1, 1)))
-k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
-            int64_t *__restrict__ Ch, int np_, int tiles_j, int rounds_per_flush)
+// Round schedule of one workgroup: classes m = 0..4 in turn; within class m
+// its digit pairs (r, m-r) and, for each, the np/64 k blocks.
+struct RoundPos {
+    int m, idx;            // class and round index inside the class
+};
+// B8: class m holds the digit pairs (r, m-r); K7: class p is the single
+// Karatsuba product of plane p with plane p.
+template <int MODE>
+__device__ __forceinline__ void class_pairs(int m, int &rlo, int &npairs)
 {
-    constexpr int K = Cfg::K, T = Cfg::T, WBI = Cfg::WBI, WBJ = Cfg::WBJ;
-    constexpr int BUF = Cfg::A_CHUNKS + Cfg::B_CHUNKS;   // 16-byte chunks per buffer
-    using RL_ = RoundLoads<Cfg>;
+    if constexpr (MODE == MFH_MODE_K7) {
+        rlo = m;
+        npairs = 1;
+    } else {
+        rlo = m > MFH_DIGITS - 1 ? m - (MFH_DIGITS - 1) : 0;
+        const int rhi = m < MFH_DIGITS - 1 ? m : MFH_DIGITS - 1;
+        npairs = rhi - rlo + 1;
+    }
+}
+
+// One workgroup: a (16*WBI) x (16*WBJ) block of elements at one evaluation
+// point, all K ring coefficients, all five digit-weight classes in turn.
+// Each class's int32 result is stored as soon as the class is complete, so
+// the only long-lived state is one int32 accumulator per (t, element); the
+// kernel fits two workgroups per CU.  Rounds are double-buffered through
+// registers: while a round's MFMAs read the LDS buffer, the next round's
+// fragments stream from global memory into VGPRs; after the round they are
+// written to LDS (one 64 KiB buffer per workgroup).
+//
+// Output C5[j][i][j'][m][t] (int32): C^_j[t] = sum_m C5[..][m][t] 2^(8m).
+// Accumulator bound: a class has at most 3 digit pairs x np/64 rounds of at
+// most K * 2^20 each; mfh_create rejects sizes where that reaches 2^31.
+template <class Cfg, int MODE>
+__global__ void __attribute__((amdgpu_flat_work_group_size(Cfg::THREADS, Cfg::THREADS),
+                               amdgpu_waves_per_eu(2, 2)))
+k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
+            int32_t *__restrict__ C5, int np_, int tiles_j)
+{
+    constexpr int K = Cfg::K, T = Cfg::T, WBI = Cfg::WBI, WBJ = Cfg::WBJ, W = Cfg::WAVES;
+    constexpr int NCLASS = MODE == MFH_MODE_K7 ? 6 : 2 * MFH_DIGITS - 1;
+    constexpr int PL = MODE == MFH_MODE_K7 ? 6 : MFH_DIGITS;     // planes per coefficient
+    constexpr int NA = K * WBI / W, NBF = K * WBJ / W;   // fragments per wave
+    static_assert((K * WBI) % W == 0 && (K * WBJ) % W == 0, "fragments split evenly");
     extern __shared__ v4i lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -206,100 +249,108 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     const int jp = blockIdx.y;
     const int i0 = ti * Cfg::BI, j0 = tj * Cfg::BJ;
     const size_t plane = (size_t)np_ * np_;
-    const int8_t *Aj = Ah + (size_t)jp * K * MFH_DIGITS * plane;
-    const int8_t *Bj = Bh + (size_t)jp * K * MFH_DIGITS * plane;
+    const int8_t *Aj = Ah + (size_t)jp * K * PL * plane;
+    const int8_t *Bj = Bh + (size_t)jp * K * PL * plane;
 
-    // this wave's load slots: fragment f = wave + WAVES*i
-    //   A: f < FA, coefficient f / WBI, row block f % WBI
-    //   B: f - FA,  coefficient (f-FA) / WBJ, column block (f-FA) % WBJ
-    const int fa = wave, fb = wave;              // first slot of each kind
-    const int8_t *a_blk = Aj + (size_t)(fa / WBI) * MFH_DIGITS * plane +
-                          (size_t)(i0 + (fa % WBI) * 16) * np_;
-    const int8_t *b_blk = Bj + (size_t)(fb / WBJ) * MFH_DIGITS * plane +
-                          (size_t)(j0 + (fb % WBJ) * 16) * np_;
-    const size_t da = (size_t)(Cfg::WAVES / WBI) * MFH_DIGITS * plane;
-    const size_t db = (size_t)(Cfg::WAVES / WBJ) * MFH_DIGITS * plane;
-    const uint32_t lane_off = (uint32_t)((lane & 15) * np_ + (lane >> 4) * 16);
-
-    long long tot[T][4];
-    v4i acc[T];
-#pragma unroll
-    for (int tt = 0; tt < T; ++tt) {
-        acc[tt] = v4i{0, 0, 0, 0};
-#pragma unroll
-        for (int v = 0; v < 4; ++v) tot[tt][v] = 0;
-    }
-
+    // this wave's fragments f = wave + W*i:
+    //   A: coefficient f / WBI, row block f % WBI
+    //   B: coefficient f / WBJ, column block f % WBJ
+    const int8_t *a_blk = Aj + (size_t)(wave / WBI) * PL * plane +
+                          (size_t)(i0 + (wave % WBI) * 16) * np_ +
+                          (lane & 15) * np_ + (lane >> 4) * 16;
+    const int8_t *b_blk = Bj + (size_t)(wave / WBJ) * PL * plane +
+                          (size_t)(j0 + (wave % WBJ) * 16) * np_ +
+                          (lane & 15) * np_ + (lane >> 4) * 16;
+    const size_t da = (size_t)(W / WBI) * PL * plane;
+    const size_t db = (size_t)(W / WBJ) * PL * plane;
+    v4i *wa = lds + wave * 64 + lane;                     // this lane's A slot of fragment f=wave
+    v4i *wbp = lds + Cfg::A_CHUNKS + wave * 64 + lane;
+    const v4i *la = lds + wbi * 64 + lane;
+    const v4i *lb = lds + Cfg::A_CHUNKS + wbj * 64 + lane;
     const int kblocks = np_ / MFH_KBLK;
-    const int rounds = MFH_DIGITS * MFH_DIGITS * kblocks;
-    auto loads_for = [&](int rd) {
-        RL_ q;
-        int r, s, m;
-        pair_of(rd / kblocks, r, s, m);
-        const int kb = rd % kblocks;
-        v4i *buf = lds + (rd & 1) * BUF;
-        q.a0 = a_blk + (size_t)r * plane + kb * MFH_KBLK;
-        q.b0 = b_blk + (size_t)s * plane + kb * MFH_KBLK;
-        q.da = da;
-        q.db = db;
-        q.lds_a = buf + fa * 64;
-        q.lds_b = buf + Cfg::A_CHUNKS + fb * 64;
-        q.lane_off = lane_off;
-        q.active = rd < rounds;
-        return q;
-    };
-    // prologue: round 0, all at once
-    {
-        RL_ q0 = loads_for(0);
-#pragma unroll
-        for (int st = 0; st < K; ++st) q0(st);
-    }
-    int since = 0;
-    auto one_round = [&](int rd, auto asc_tag) {
-        constexpr bool ASC = decltype(asc_tag)::value;
-        const v4i *cur = lds + (rd & 1) * BUF;
-        // this round's tiles have landed (own loads), and every wave is done
-        // with the buffer the next round's loads overwrite
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        const RL_ q = loads_for(rd + 1);
-        const v4i *la = cur + wbi * 64 + lane;
-        const v4i *lb = cur + Cfg::A_CHUNKS + wbj * 64 + lane;
-        pw_dispatch<Cfg, ASC>(tg, acc, la, lb, q);
-        ++since;
-        int r, s, m, rn, sn, mn;
-        pair_of(rd / kblocks, r, s, m);
-        const bool last = rd + 1 == rounds;
-        mn = m;
-        if (!last) pair_of((rd + 1) / kblocks, rn, sn, mn);
-        if (last || mn != m || since == rounds_per_flush) {
-            // after an ascending round acc = -(P-N), after a descending one +(P-N)
-            const long long w = (ASC ? -1LL : 1LL) << (8 * m);
-#pragma unroll
-            for (int tt = 0; tt < T; ++tt) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) tot[tt][v] += (long long)acc[tt][v] * w;
-                acc[tt] = v4i{0, 0, 0, 0};
-            }
-            since = 0;
-        }
-    };
-    int rd = 0;
-    for (; rd + 1 < rounds; rd += 2) {
-        one_round(rd, std::true_type{});
-        one_round(rd + 1, std::false_type{});
-    }
-    if (rd < rounds) one_round(rd, std::true_type{});
-
-    // epilogue: lane holds rows 4*(lane/16)+v, column lane%16 of its block
     const int col = j0 + wbj * 16 + (lane & 15);
+    int32_t *out_base = C5 + (((size_t)jp * np_ + i0 + wbi * 16 + 4 * (lane >> 4)) * np_ + col) *
+                                 (NCLASS * K) + tg * T;
+
+    v4i R[NA + NBF];
+    auto gload = [&](RoundPos q) {
+        int rlo, np2;
+        class_pairs<MODE>(q.m, rlo, np2);
+        const int r = rlo + q.idx / kblocks, kb = q.idx % kblocks;
+        const int s = MODE == MFH_MODE_K7 ? r : q.m - r;
+        const int8_t *a0 = a_blk + (size_t)r * plane + kb * MFH_KBLK;
+        const int8_t *b0 = b_blk + (size_t)s * plane + kb * MFH_KBLK;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const int row = i0 + wbi * 16 + 4 * (lane >> 4) + v;
-        long long *dst = (long long *)Ch + (((size_t)jp * np_ + row) * np_ + col) * K + tg * T;
+        for (int i = 0; i < NA; ++i) R[i] = *(const v4i *)(a0 + i * da);
 #pragma unroll
-        for (int tt = 0; tt < T; tt += 2)
-            *(longlong2 *)(dst + tt) = make_longlong2(tot[tt][v], tot[tt + 1][v]);
+        for (int i = 0; i < NBF; ++i) R[NA + i] = *(const v4i *)(b0 + i * db);
+    };
+    auto lwrite = [&]() {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) wa[i * W * 64] = R[i];
+#pragma unroll
+        for (int i = 0; i < NBF; ++i) wbp[i * W * 64] = R[NA + i];
+    };
+    auto next_of = [&](RoundPos q) {
+        int rlo, np2;
+        class_pairs<MODE>(q.m, rlo, np2);
+        if (q.idx + 1 < np2 * kblocks) return RoundPos{q.m, q.idx + 1};
+        return RoundPos{q.m + 1, 0};
+    };
+
+    // prologue: round (0,0) into LDS, round after it into registers
+    RoundPos cur{0, 0};
+    gload(cur);
+    lwrite();
+    RoundPos nxt = next_of(cur);
+    gload(nxt);
+    __syncthreads();
+
+    v4i acc[T];
+    // one round: MFMAs from LDS, then hand the registers' round to LDS and
+    // start loading the one after
+    auto step = [&](auto asc_tag) {
+        constexpr bool ASC = decltype(asc_tag)::value;
+        pw_dispatch<Cfg, ASC>(tg, acc, la, lb, NoIssue{});
+        __syncthreads();                     // every wave is done reading LDS
+        cur = nxt;
+        if (cur.m < NCLASS) {
+            lwrite();                        // waits for the registers' loads
+            nxt = next_of(cur);
+            if (nxt.m < NCLASS) gload(nxt);
+        }
+        __syncthreads();
+    };
+#pragma unroll 1
+    for (int m = 0; m < NCLASS; ++m) {
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) acc[tt] = v4i{0, 0, 0, 0};
+        int rlo, np2;
+        class_pairs<MODE>(m, rlo, np2);
+        const int rounds = np2 * kblocks;
+        int rd = 0;
+#pragma unroll 1
+        for (; rd + 1 < rounds; rd += 2) {
+            step(std::true_type{});
+            step(std::false_type{});
+        }
+        // after an ascending round the accumulator holds -(P-N)
+        const bool flip = rd < rounds;
+        if (flip) step(std::true_type{});
+        // store this class: rows 4*(lane/16)+v, column lane%16, T values of t
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            int32_t *dst = out_base + (size_t)v * np_ * (NCLASS * K) + m * K;
+#pragma unroll
+            for (int tt = 0; tt < T; tt += 4) {
+                int4 q;
+                q.x = flip ? -acc[tt][v] : acc[tt][v];
+                q.y = flip ? -acc[tt + 1][v] : acc[tt + 1][v];
+                q.z = flip ? -acc[tt + 2][v] : acc[tt + 2][v];
+                q.w = flip ? -acc[tt + 3][v] : acc[tt + 3][v];
+                *(int4 *)(dst + tt) = q;
+            }
+        }
     }
 }
 
@@ -309,15 +360,21 @@ int launch_cfg(mfh_ctx *c)
     const int tiles_i = c->np / Cfg::BI, tiles_j = c->np / Cfg::BJ;
     static bool attr_set = false;
     if (!attr_set) {
-        MFH_HIP(hipFuncSetAttribute((const void *)k_pointwise<Cfg>,
+        MFH_HIP(hipFuncSetAttribute((const void *)k_pointwise<Cfg, MFH_MODE_B8>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    Cfg::LDS_BYTES));
+        MFH_HIP(hipFuncSetAttribute((const void *)k_pointwise<Cfg, MFH_MODE_K7>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
                                     Cfg::LDS_BYTES));
         attr_set = true;
     }
     dim3 grid((unsigned)(tiles_i * tiles_j), (unsigned)c->NB);
-    hipLaunchKernelGGL(k_pointwise<Cfg>, grid, dim3(Cfg::THREADS), Cfg::LDS_BYTES,
-                       c->stream, c->dAh, c->dBh, c->dCh, c->np, tiles_j,
-                       mfh_rounds_per_flush(c->K));
+    if (c->mode == MFH_MODE_K7)
+        hipLaunchKernelGGL((k_pointwise<Cfg, MFH_MODE_K7>), grid, dim3(Cfg::THREADS),
+                           Cfg::LDS_BYTES, c->stream, c->dAh, c->dBh, c->dC5, c->np, tiles_j);
+    else
+        hipLaunchKernelGGL((k_pointwise<Cfg, MFH_MODE_B8>), grid, dim3(Cfg::THREADS),
+                           Cfg::LDS_BYTES, c->stream, c->dAh, c->dBh, c->dC5, c->np, tiles_j);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }

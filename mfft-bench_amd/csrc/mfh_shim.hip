@@ -61,6 +61,26 @@ int ensure_staging(mfh_ctx *c, size_t in_bytes, size_t out_bytes)
     return MFH_OK;
 }
 
+// Digit mode of a product.  K7 (6 Karatsuba products instead of 9) needs
+// every transformed value inside [-1056832, 1040319]: without recoding
+// |a^| <= (NB/2) 65535; the exact track's forward transform can first
+// recode limbs to [-2^15, 2^15) (top limb <= 2^16), giving
+// |a^| <= (NB/2 + 1) 2^15, for the plans it is specialised for.  conv_mfft
+// must return the convolution of the caller's limbs, so it never recodes.
+bool k7_plain(const mfh_ctx *c) { return (long long)(c->NB / 2) * 65535 <= MFH_K7_MAX; }
+bool k7_recoded(const mfh_ctx *c)
+{
+    return c->use_fast && c->n % 8 == 0 && c->S == 8 && c->NB == 32 &&
+           (long long)(c->NB / 2 + 1) * 32768 <= MFH_K7_MAX;
+}
+void select_mode(mfh_ctx *c, bool exact_track)
+{
+    c->recode = 0;
+    if (k7_plain(c)) c->mode = MFH_MODE_K7;
+    else if (exact_track && k7_recoded(c)) { c->mode = MFH_MODE_K7; c->recode = 1; }
+    else c->mode = MFH_MODE_B8;
+}
+
 void mark(mfh_ctx *c, int k)
 {
     if (c->timing) (void)hipEventRecord(c->ev[k], c->stream);
@@ -141,6 +161,7 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     double bits = log2((double)p->NB) + log2((double)p->K) + log2((double)np_) +
                   2.0 * log2((double)(p->NB / 2) * 65535.0);
     if (bits >= 62.0) return MFH_E_BOUND;
+    if (!mfh_class_bound_ok(p->K, np_)) return MFH_E_BOUND;
     int rc = check_device();
     if (rc) return rc;
 
@@ -155,10 +176,15 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     }
     for (int k = 0; k < 5; ++k) (void)hipEventCreate(&c->ev[k]);
     const size_t nnp = (size_t)np_ * np_, nn = (size_t)n * n;
-    const size_t digit_bytes = (size_t)c->NB * c->K * MFH_DIGITS * nnp;
+    c->k7_ok = k7_plain(c) || k7_recoded(c);
+    const int planes = c->k7_ok ? MFH_PLANES_MAX : MFH_DIGITS;
+    const int classes = c->k7_ok ? MFH_CLASSES_MAX : MFH_CLASSES;
+    select_mode(c, true);
+    const size_t digit_bytes = (size_t)c->NB * c->K * planes * nnp;
     rc = dalloc(c, (void **)&c->dAh, digit_bytes);
     if (!rc) rc = dalloc(c, (void **)&c->dBh, digit_bytes);
-    if (!rc) rc = dalloc(c, (void **)&c->dCh, (size_t)c->NB * c->K * nnp * sizeof(int64_t));
+    if (!rc) rc = dalloc(c, (void **)&c->dC5,
+                         (size_t)c->NB * classes * c->K * nnp * sizeof(int32_t));
     if (!rc) rc = dalloc(c, (void **)&c->dCw, (size_t)(2 * L - 1) * nn * sizeof(int64_t));
     if (!rc) rc = dalloc(c, &c->dBt, (size_t)L * nn * sizeof(int32_t));
     if (!rc) rc = dalloc(c, (void **)&c->dFlag, sizeof(int));
@@ -171,7 +197,7 @@ void mfh_destroy(mfh_ctx *c)
 {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
-    void *bufs[] = {c->dAh, c->dBh, c->dCh, c->dCw, c->dBt, c->dFlag,
+    void *bufs[] = {c->dAh, c->dBh, c->dC5, c->dCw, c->dBt, c->dFlag,
                     c->dInA, c->dInB, c->dOut};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
@@ -187,6 +213,7 @@ int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut,
 {
     if (!c || !dA || !dB || !dOut || RL < 1) return MFH_E_ARG;
     if (kind != MFH_IN_U16 && kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
+    select_mode(c, true);
     int rc = run_conv(c, kind, dA, dB, c->dCw, 0, 0);
     if (rc) return rc;
     if ((rc = mfh_launch_carry(c, c->dCw, (uint16_t *)dOut, RL))) return rc;
@@ -203,6 +230,7 @@ int mfh_conv_dev(mfh_ctx *c, const void *dA32, const void *dB32, void *dCw)
     if ((rc = mfh_launch_check_i32(c, (const int32_t *)dB32, c->L))) return rc;
     if ((rc = read_flag(c, &flag))) return rc;
     if (flag) return MFH_E_RANGE;
+    select_mode(c, false);
     rc = run_conv(c, MFH_IN_I32, dA32, dB32, (int64_t *)dCw, 0, 0);
     if (rc) return rc;
     mark(c, 4);
@@ -212,6 +240,7 @@ int mfh_conv_dev(mfh_ctx *c, const void *dA32, const void *dB32, void *dCw)
 int mfh_fpx_mm_dev(mfh_ctx *c, const void *dA, const void *dB, int SA, int SB, void *dC)
 {
     if (!c || !dA || !dB || !dC) return MFH_E_ARG;
+    select_mode(c, false);
     int rc = run_conv(c, MFH_IN_F32, dA, dB, c->dCw, SA, SB);
     if (rc) return rc;
     if ((rc = mfh_launch_decode_f32(c, c->dCw, SA + SB, (float *)dC))) return rc;
@@ -337,9 +366,10 @@ int mfh_work(const mfh_ctx *c, double *ops, double *fwd, double *inv)
     if (!c) return MFH_E_ARG;
     const double nnp = (double)c->np * c->np, nn = (double)c->n * c->n;
     const double pts = (double)c->NB * c->K;
-    if (ops) *ops = 2.0 * MFH_DIGITS * MFH_DIGITS * c->NB * (double)c->K * c->K * nnp * c->np;
-    if (fwd) *fwd = 2.0 * ((double)c->L * nn * 2.0 + pts * MFH_DIGITS * nnp);
-    if (inv) *inv = pts * nnp * 8.0 + (2.0 * c->L - 1.0) * nn * 8.0;
+    const double products = c->mode == MFH_MODE_K7 ? 6.0 : 9.0;
+    if (ops) *ops = 2.0 * products * c->NB * (double)c->K * c->K * nnp * c->np;
+    if (fwd) *fwd = 2.0 * ((double)c->L * nn * 2.0 + pts * mfh_planes(c->mode) * nnp);
+    if (inv) *inv = pts * nnp * 4.0 * mfh_nclasses(c->mode) + (2.0 * c->L - 1.0) * nn * 8.0;
     return MFH_OK;
 }
 

@@ -74,12 +74,48 @@ struct SrcF32 {
     }
 };
 
-__device__ __forceinline__ void split3(int v, int &d0, int &d1, int &d2)
+
+// C^ from the pointwise step's int32 class results (stride K between
+// classes): B8 sum_m class_m 2^(8m); K7 the Karatsuba recombination
+__device__ __forceinline__ long long combine_classes(const int32_t *p, int K, int mode)
 {
-    d0 = (v << 24) >> 24;          // sign-extended low byte
-    int v1 = (v - d0) >> 8;        // exact
-    d1 = (v1 << 24) >> 24;
-    d2 = (v1 - d1) >> 8;           // in [-128, 127] by the plan bound
+    if (mode == MFH_MODE_K7) {
+        const long long P0 = p[0], P1 = p[K], P2 = p[2 * K], P3 = p[3 * K], P4 = p[4 * K],
+                        P5 = p[5 * K];
+        const long long c1 = P3 - P0 - P1, c2 = P4 - P0 - P2 + P1, c3 = P5 - P1 - P2;
+        return P0 + c1 * 128 + c2 * 16384 + c3 * 2097152 + P2 * 268435456;
+    }
+    long long v = 0;
+#pragma unroll
+    for (int m = MFH_CLASSES - 1; m >= 0; --m) v = v * 256 + (long long)p[m * K];
+    return v;
+}
+
+// Digit planes of one transformed value v (plane stride nnp):
+//  B8: balanced base-2^8 digits, i.e. the low bytes of v, (v + 2^7) >> 8 and
+//      (v + 2^15 + 2^7) >> 16 (each the floor that makes the lower digits
+//      land in [-128, 127]).
+//  K7: balanced base-2^7 digits d0, d1, d2 in [-64, 63] and the sums
+//      d0+d1, d0+d2, d1+d2.
+template <int MODE>
+__device__ __forceinline__ void store_digits(int8_t *p, size_t nnp, int v)
+{
+    if constexpr (MODE == MFH_MODE_B8) {
+        p[0] = (int8_t)v;
+        p[nnp] = (int8_t)((v + 128) >> 8);
+        p[2 * nnp] = (int8_t)((v + 32896) >> 16);
+    } else {
+        const int d0 = ((v + 64) & 127) - 64;
+        const int v1 = (v + 64) >> 7;
+        const int d1 = ((v1 + 64) & 127) - 64;
+        const int d2 = (v1 + 64) >> 7;
+        p[0] = (int8_t)d0;
+        p[nnp] = (int8_t)d1;
+        p[2 * nnp] = (int8_t)d2;
+        p[3 * nnp] = (int8_t)(d0 + d1);
+        p[4 * nnp] = (int8_t)(d0 + d2);
+        p[5 * nnp] = (int8_t)(d1 + d2);
+    }
 }
 
 // ---- forward transform, generic plan ---------------------------------------
@@ -87,7 +123,7 @@ __device__ __forceinline__ void split3(int v, int &d0, int &d1, int &d2)
 // three digit planes of every (point j, coefficient c).  Elements outside
 // the n x n input are zero.  Output plane (j, c, r) holds digit r of X[j][c]
 // as an np x np row-major int8 matrix.
-template <class Src>
+template <class Src, int MODE>
 __global__ __launch_bounds__(256) void k_forward_generic(
     Src src, int8_t *__restrict__ out, int np_, int LS, int S, int NB, int K,
     int g)
@@ -110,12 +146,8 @@ __global__ __launch_bounds__(256) void k_forward_generic(
                     else if (s >= K && s < K + S) acc -= src.get(b * S + s - K, i, k);
                 }
             }
-            int d0, d1, d2;
-            split3(acc, d0, d1, d2);
-            int8_t *o = out + ((size_t)(j * K + c) * MFH_DIGITS) * nnp + e;
-            o[0] = (int8_t)d0;
-            o[nnp] = (int8_t)d1;
-            o[2 * nnp] = (int8_t)d2;
+            constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
+            store_digits<MODE>(out + ((size_t)(j * K + c) * PL) * nnp + e, nnp, acc);
         }
     }
 }
@@ -156,9 +188,13 @@ template <int L>
 struct LimbsLds {
     const uint32_t *base;      // lds + thread slot
     bool top_signed;
+    bool recoded;              // pairs hold signed int16 limbs, top in `top`
+    int top;
     __device__ __forceinline__ int get(int u) const
     {
+        if (recoded && u == L - 1) return top;
         const uint32_t w = base[(u / 2) * 256];
+        if (recoded) return (u & 1) ? (int)(short)(w >> 16) : (int)(short)(w & 0xFFFFu);
         if (u == L - 1 && top_signed) return (int)(short)(w >> 16);
         return (u & 1) ? (int)(w >> 16) : (int)(w & 0xFFFFu);
     }
@@ -210,18 +246,11 @@ __device__ __forceinline__ void load_limbs(LimbsI32<L> &x, const Src &src, int i
     for (int u = 0; u < L; ++u) x.r[u] = valid ? src.get(u, i, k) : 0;
 }
 
-// balanced base-2^8 digits of v: bytes of v, (v + 2^7) >> 8, (v + 2^15 + 2^7) >> 16
-__device__ __forceinline__ void store_digits(int8_t *p, size_t nnp, int v)
-{
-    p[0] = (int8_t)v;
-    p[nnp] = (int8_t)((v + 128) >> 8);
-    p[2 * nnp] = (int8_t)((v + 32896) >> 16);
-}
-
 // One output class q (compile time): twist + fold, length-P DIF, digits.
-template <int S, int NB, int Q, int q, class Limbs>
+template <int S, int NB, int Q, int q, int MODE, class Limbs>
 __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t nnp)
 {
+    constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
     constexpr int K = 2 * S, P = NB / Q, LS = NB / 2;
     constexpr int g = 2 * K / NB, twoK = 2 * K;
     int z[P][K];
@@ -275,18 +304,18 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
         const int j = q + Q * jp;
 #pragma unroll
         for (int c = 0; c < K; ++c)
-            store_digits(o + (size_t)((j * K + c) * MFH_DIGITS) * nnp, nnp, z[pos][c]);
+            store_digits<MODE>(o + (size_t)((j * K + c) * PL) * nnp, nnp, z[pos][c]);
     }
 }
 
-template <int S, int NB, int Q, class Limbs, int... qs>
+template <int S, int NB, int Q, int MODE, class Limbs, int... qs>
 __device__ __forceinline__ void forward_classes(const Limbs &x, int8_t *o, size_t nnp,
                                                 std::integer_sequence<int, qs...>)
 {
-    (forward_class<S, NB, Q, qs, Limbs>(x, o, nnp), ...);
+    (forward_class<S, NB, Q, qs, MODE, Limbs>(x, o, nnp), ...);
 }
 
-template <int S, int NB, int Q, class Limbs, class Src>
+template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src>
 __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restrict__ out, int np_,
                                                       int top_signed)
 {
@@ -301,6 +330,31 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
         __syncthreads();
         x.base = stage + threadIdx.x;
         x.top_signed = top_signed != 0;
+        x.recoded = RECODE;
+        if constexpr (RECODE) {
+            // Signed recoding y_u = x_u + c_u - 2^16 c_(u+1) with
+            // c_(u+1) = [x_u + c_u >= 2^15]: the same integer, limbs below
+            // the top in [-2^15, 2^15), the top limb x + c unrecoded.  This
+            // halves the bound on the transformed values.
+            uint32_t *slot = stage + threadIdx.x;
+            int carry = 0;
+#pragma unroll 8
+            for (int p2 = 0; p2 < L / 2; ++p2) {
+                const uint32_t w = slot[p2 * 256];
+                int lo = (int)(w & 0xFFFFu) + carry;
+                carry = lo >= 32768;
+                lo -= carry << 16;
+                int hi = (int)(w >> 16) + carry;
+                if (p2 + 1 < L / 2) {
+                    carry = hi >= 32768;
+                    hi -= carry << 16;
+                } else {
+                    x.top = top_signed ? (int)(short)(w >> 16) + carry : hi;
+                    hi = 0;
+                }
+                slot[p2 * 256] = ((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16);
+            }
+        }
         if (e >= nnp) return;
     } else {
         if (e >= nnp) return;
@@ -309,7 +363,7 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
         load_limbs<L>(x, src, i, k, valid);
         if constexpr (std::is_same_v<Limbs, LimbsPacked<L>>) x.top_signed = top_signed != 0;
     }
-    forward_classes<S, NB, Q, Limbs>(x, out + e, nnp, std::make_integer_sequence<int, Q>{});
+    forward_classes<S, NB, Q, MODE, Limbs>(x, out + e, nnp, std::make_integer_sequence<int, Q>{});
 }
 
 // |limb| <= 65535 for int32 inputs (the transform and digit bounds assume it)
@@ -333,10 +387,10 @@ __global__ __launch_bounds__(256) void k_check_i32(const int32_t *p, size_t coun
 // Cooley-Tukey stages len = 2..NB with conjugate twiddles give NB * x_b in
 // natural order (the semantics of src/mfft.c:260-299).  Fold:
 //     Cw[b*S + c] = x_b[c] + x_(b-1)[c + S],  c < S   (src/mfft.c:407-418)
-__global__ void k_inverse_fold(const int64_t *__restrict__ Ch,
+__global__ void k_inverse_fold(const int32_t *__restrict__ C5,
                                int64_t *__restrict__ Cw, int n, int np_,
                                int NB, int K, int S, int g, int lgNB, int P,
-                               int epw)
+                               int epw, int mode, int ncl)
 {
     extern __shared__ int64_t sm[];
     const int tid = threadIdx.x;
@@ -351,7 +405,8 @@ __global__ void k_inverse_fold(const int64_t *__restrict__ Ch,
     if (valid) {
         for (int j = 0; j < NB; ++j) {
             const int r = lgNB ? (int)(__brev((unsigned)j) >> (32 - lgNB)) : 0;
-            X[r * K + c] = Ch[(((size_t)j * np_ + i) * np_ + jj) * K + c];
+            X[r * K + c] = combine_classes(C5 + (((size_t)j * np_ + i) * np_ + jj) * (ncl * K) + c,
+                                           K, mode);
         }
     }
     __syncthreads();
@@ -403,9 +458,9 @@ __device__ __forceinline__ long long bperm64(long long v, int addr)
 }
 
 template <int NB, int K>
-__global__ __launch_bounds__(256) void k_inverse_fast(const int64_t *__restrict__ Ch,
+__global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict__ C5,
                                                       int64_t *__restrict__ Cw, int n, int np_,
-                                                      int P)
+                                                      int P, int mode, int ncl)
 {
     constexpr int S = K / 2, g = 2 * K / NB, twoK = 2 * K;
     constexpr int PASS = 256 / K;            // elements per pass
@@ -430,7 +485,9 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int64_t *__restrict_
 #pragma unroll
             for (int bit = 1, rb = NB >> 1; bit < NB; bit <<= 1, rb >>= 1)
                 if (j & bit) r |= rb;
-            X[r] = valid ? Ch[(((size_t)j * np_ + i) * np_ + jj) * K + c] : 0;
+            X[r] = valid ? combine_classes(C5 + (((size_t)j * np_ + i) * np_ + jj) * (ncl * K) + c,
+                                           K, mode)
+                         : 0;
         }
 #pragma unroll
         for (int len = 2; len <= NB; len <<= 1) {
@@ -661,12 +718,12 @@ int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
 
 namespace {
 // compile-time plans: (S, NB) with the class count Q = NB/4
-template <int S, int NB, class Src, class Limbs>
+template <int S, int NB, int MODE, bool RECODE, class Src, class Limbs>
 bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_signed)
 {
-    if (c->S != S || c->NB != NB) return false;
+    if (c->S != S || c->NB != NB || c->mode != MODE || (c->recode != 0) != RECODE) return false;
     const size_t nnp = (size_t)c->np * c->np;
-    hipLaunchKernelGGL((k_forward_fast<S, NB, NB / 4, Limbs, Src>),
+    hipLaunchKernelGGL((k_forward_fast<S, NB, NB / 4, MODE, RECODE, Limbs, Src>),
                        dim3((unsigned)((nnp + 255) / 256)), dim3(256), 0, c->stream, s, dst,
                        c->np, top_signed);
     return true;
@@ -674,12 +731,25 @@ bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_signed)
 
 bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int top_signed)
 {
+    constexpr int K7 = MFH_MODE_K7, B8 = MFH_MODE_B8;
     if (c->n % 8) return false;   // staged 16-byte loads need rows of 8k limbs
-    return try_fast<8, 32, SrcU16, LimbsLds<128>>(c, s, dst, top_signed) ||   // W=2048
-           try_fast<8, 16, SrcU16, LimbsLds<64>>(c, s, dst, top_signed) ||    // W=1024
-           try_fast<4, 16, SrcU16, LimbsPacked<32>>(c, s, dst, top_signed);   // W=512
+    return try_fast<8, 32, K7, true, SrcU16, LimbsLds<128>>(c, s, dst, top_signed) ||  // W=2048
+           try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>>(c, s, dst, top_signed) ||
+           try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>>(c, s, dst, top_signed) ||  // W=1024
+           try_fast<4, 16, K7, false, SrcU16, LimbsPacked<32>>(c, s, dst, top_signed); // W=512
 }
 }  // namespace
+
+template <class Src>
+void launch_generic(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid, int LS)
+{
+    if (c->mode == MFH_MODE_K7)
+        hipLaunchKernelGGL((k_forward_generic<Src, MFH_MODE_K7>), grid, dim3(256), 0, c->stream,
+                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+    else
+        hipLaunchKernelGGL((k_forward_generic<Src, MFH_MODE_B8>), grid, dim3(256), 0, c->stream,
+                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+}
 
 int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
                        int scale_S)
@@ -695,7 +765,7 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
             done = forward_fast_u16(c, s, dst, in_kind == MFH_IN_U16_SIGNED);
         } else if (in_kind == MFH_IN_F32) {
             SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
-            done = try_fast<4, 16, SrcF32, LimbsI32<32>>(c, s, dst, 0);       // 512-bit grid
+            done = try_fast<4, 16, MFH_MODE_K7, false, SrcF32, LimbsI32<32>>(c, s, dst, 0);
         }
         if (done) {
             MFH_HIP(hipGetLastError());
@@ -705,26 +775,22 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
     switch (in_kind) {
     case MFH_IN_U16: {
         SrcU16 s{(const uint16_t *)src, nn, c->n, c->L};
-        hipLaunchKernelGGL(k_forward_generic<SrcU16>, grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+        launch_generic<SrcU16>(c, s, dst, grid, LS);
         break;
     }
     case MFH_IN_U16_SIGNED: {
         SrcU16Signed s{(const uint16_t *)src, nn, c->n, c->L};
-        hipLaunchKernelGGL(k_forward_generic<SrcU16Signed>, grid, dim3(256), 0,
-                           c->stream, s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+        launch_generic<SrcU16Signed>(c, s, dst, grid, LS);
         break;
     }
     case MFH_IN_I32: {
         SrcI32 s{(const int32_t *)src, nn, c->n, c->L};
-        hipLaunchKernelGGL(k_forward_generic<SrcI32>, grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+        launch_generic<SrcI32>(c, s, dst, grid, LS);
         break;
     }
     case MFH_IN_F32: {
         SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
-        hipLaunchKernelGGL(k_forward_generic<SrcF32>, grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+        launch_generic<SrcF32>(c, s, dst, grid, LS);
         break;
     }
     default:
@@ -762,7 +828,8 @@ bool try_inverse_fast(mfh_ctx *c, int64_t *Cw)
     }
     const size_t nn = (size_t)c->n * c->n;
     hipLaunchKernelGGL((k_inverse_fast<NB, K>), dim3((unsigned)((nn + E - 1) / E)), dim3(256),
-                       lds, c->stream, c->dCh, Cw, c->n, c->np, P);
+                       lds, c->stream, c->dC5, Cw, c->n, c->np, P, c->mode,
+                       mfh_nclasses(c->mode));
     return true;
 }
 }  // namespace
@@ -792,8 +859,8 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw)
     }
     dim3 grid((unsigned)((nn + epw - 1) / epw));
     hipLaunchKernelGGL(k_inverse_fold, grid, dim3(threads), lds, c->stream,
-                       c->dCh, Cw, c->n, c->np, c->NB, c->K, c->S, c->g,
-                       lg2i(c->NB), 2 * c->L - 1, epw);
+                       c->dC5, Cw, c->n, c->np, c->NB, c->K, c->S, c->g,
+                       lg2i(c->NB), 2 * c->L - 1, epw, c->mode, mfh_nclasses(c->mode));
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }
