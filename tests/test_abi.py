@@ -1,0 +1,140 @@
+"""The C-ABI library: it loads without a GPU, exports every function the
+public headers declare, and its host-side logic (plan, sizing, argument and
+bound checks, error conventions) matches the reference without any compute
+call."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("mfftbench.h", "mfft_hip.h")]
+
+
+def declared_functions(path):
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    names = set()
+    for m in re.finditer(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\(([^;{}]*)\)\s*;", text):
+        name = m.group(1)
+        if name in {"if", "while", "sizeof", "return"}:
+            continue
+        names.add(name)
+    return names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    import mfft_ctypes
+    out = subprocess.run(["nm", "-D", "--defined-only", mfft_ctypes.LIB_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    declared = set()
+    for h in HEADERS:
+        declared |= declared_functions(h)
+    assert len(declared) > 40
+    missing = sorted(declared - exported)
+    assert not missing, f"declared but not exported: {missing}"
+    for name in declared:
+        getattr(lib, name)                               # resolvable through ctypes
+
+
+def test_no_internal_symbols_leak():
+    import mfft_ctypes
+    out = subprocess.run(["nm", "-D", "--defined-only", mfft_ctypes.LIB_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    names = [line.split()[-1] for line in out.splitlines() if " T " in line]
+    assert not [n for n in names if n.startswith("_Z")], "C++ internals exported"
+
+
+def test_loads_without_device(lib):
+    assert lib.mfh_device_count() >= 0
+    assert isinstance(lib.mfh_device_arch(), bytes)
+
+
+def test_plan_matches_oracle(lib, orc):
+    import mfft_ctypes as M
+    for L in [2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048]:
+        for sigma in [0, 1, 2, 3, 4, 5]:
+            p = M.plan(L, sigma)
+            q = orc.plan(L, sigma)
+            assert (p is None) == (q is None), (L, sigma)
+            if p is not None:
+                assert (p.L, p.S, p.NB, p.K, p.g, p.nprod) == (q.L, q.S, q.NB, q.K, q.g, q.nprod)
+                assert lib.mfft_plan_products(C.byref(p)) == q.nprod
+                assert lib.mfft_plan_maxbits(C.byref(p), 64) == pytest.approx(
+                    orc.lib.orc_plan_maxbits(C.byref(q), 64))
+    assert M.plan(96) is None and M.plan(0) is None
+
+
+def test_kernel_names(lib):
+    assert lib.kernel_name(2) == b"packed" and lib.kernel_name(12) == b"hip"
+    assert lib.kernel_from_name(b"hip") == 12 and lib.kernel_from_name(b"ikj") == 0
+    assert lib.kernel_from_name(b"nope") == -1
+
+
+def test_host_generator_and_compare(lib, orc):
+    n, L = 7, 9
+    m = np.empty(L * n * n, np.uint16)
+    lib.bigmat_rand(m.ctypes.data, n, L, 4242)
+    assert np.array_equal(m, orc.bigmat_rand(n, L, 4242))
+    b = m.copy()
+    bi, bj, bw = C.c_int(), C.c_int(), C.c_int()
+    assert lib.bigres_equal(m.ctypes.data, b.ctypes.data, n, L, None, None, None) == 1
+    b[3 * n * n + 2 * n + 5] ^= 1
+    assert lib.bigres_equal(m.ctypes.data, b.ctypes.data, n, L,
+                            C.byref(bi), C.byref(bj), C.byref(bw)) == 0
+    assert (bi.value, bj.value, bw.value) == (2, 5, 3)
+
+
+def test_cpu_leaf_is_refused_output_untouched(lib):
+    """Only KERNEL_HIP runs: a CPU leaf is an error, never a fallback
+    (src/mfft.c:432 convention: output left untouched)."""
+    import mfft_ctypes as M
+    n, L = 4, 8
+    A = np.ones(L * n * n, np.uint16)
+    out, err = M.mm_mfft(A, A, n, L, M.plan(L), kernel=M.KERNEL_PACKED)
+    assert err == -7 and not out.any()
+    cw, err = M.conv_mfft(A.astype(np.int32), A.astype(np.int32), n, L, M.plan(L),
+                          kernel=M.KERNEL_PACKED)
+    assert err == -7 and not cw.any()
+
+
+def test_create_checks_arguments_and_bounds(lib):
+    import mfft_ctypes as M
+    h = C.c_void_p()
+    p = M.plan(128)
+    assert lib.mfh_create(C.byref(h), 0, 128, C.byref(p)) == -3          # n < 1
+    bad = M.Plan(L=128, S=8, NB=32, K=16, g=2, rec=0, nprod=0)          # wrong g
+    assert lib.mfh_create(C.byref(h), 64, 128, C.byref(bad)) == -3
+    assert lib.mfh_create(C.byref(h), 64, 64, C.byref(p)) == -3         # L mismatch
+    p1k = M.plan(1024)                                                  # K = 64
+    assert lib.mfh_create(C.byref(h), 64, 1024, C.byref(p1k)) == -7
+    # int32 class accumulators: 3 * (np/64) * K * 2^20 must stay below 2^31
+    assert lib.mfh_create(C.byref(h), 8192, 128, C.byref(p)) == -4
+    if lib.mfh_device_count() == 0:
+        assert lib.mfh_create(C.byref(h), 64, 128, C.byref(p)) == -1    # no device
+        assert not h.value
+
+
+def test_fpx_init_sizing_matches_reference_rules(lib, orc):
+    import mfft_ctypes as M
+    n = 6
+    A = orc.fp32_rand(n * n, 1, -20, 20)
+    B = orc.fp32_rand(n * n, 2, -5, 9)
+    for force in (512, 0):
+        ctx = M.FpxCtx()
+        assert lib.fpx_init(C.byref(ctx), A.ctypes.data, B.ctypes.data, n, force) == 0
+        oc = orc.fpx(A, B, n, force)
+        assert (ctx.L, ctx.SA, ctx.SB, ctx.spreadA, ctx.spreadB) == \
+               (oc.L, oc.SA, oc.SB, oc.spreadA, oc.spreadB)
+        lib.fpx_free(C.byref(ctx))
+        orc.fpx_free(oc)
+    # src/fpfixed.c:84-88 overflow guard
+    nb = 1024                                   # n * L * 65535^2 > 4e18 at L = 2^20
+    big = np.ones(nb * nb, np.float32)
+    ctx = M.FpxCtx()
+    assert lib.fpx_init(C.byref(ctx), big.ctypes.data, big.ctypes.data, nb, 1 << 24) == -1

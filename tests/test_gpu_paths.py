@@ -1,0 +1,261 @@
+"""GPU parity of every entry point, through the C-ABI: conv_mfft on signed
+limbs, two's complement products, the fp32 embedding, device normalize /
+encode / decode, the device input generator, the generic (runtime-plan)
+kernels, and the full-size workloads checked by Freivalds' test plus exact
+sampled entries."""
+import ctypes as C
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+SEED, SEED_B = 12345, 12345 ^ 0xABCDEF
+
+
+def signed_limbs(orc, n, L, seed):
+    A = orc.bigmat_rand(n, L, seed)
+    top = slice((L - 1) * n * n, L * n * n)
+    A32 = A.astype(np.int32)
+    A32[top] = A[top].view(np.int16)
+    return A, A32
+
+
+# ---- conv_mfft: the convolution of the caller's limbs --------------------------
+@pytest.mark.parametrize("n,L,sigma", [(6, 8, 0), (16, 32, 0), (9, 32, 3), (40, 64, 0),
+                                       (24, 128, 0), (5, 512, 0)])
+def test_conv_signed_limbs(gpu, orc, n, L, sigma):
+    print(f"[conv] n={n} L={L}", flush=True)
+    rng = np.random.default_rng(n * L)
+    A = rng.integers(-65535, 65536, size=L * n * n).astype(np.int32)
+    B = rng.integers(-65535, 65536, size=L * n * n).astype(np.int32)
+    A[:n * n] = 65535                                   # worst-case magnitudes
+    B[:n * n] = -65535
+    want = orc.conv_limbplane(A, B, n, L)
+    with gpu.Ctx(n, L, gpu.plan(L, sigma)) as ctx:
+        got = ctx.conv(A, B)
+    assert np.array_equal(got, want)
+
+
+def test_conv_rejects_out_of_range_limb(gpu):
+    n, L = 8, 16
+    A = np.zeros(L * n * n, np.int32)
+    A[5] = 65536
+    with gpu.Ctx(n, L) as ctx:
+        with pytest.raises(gpu.MfftError) as e:
+            ctx.conv(A, A)
+    assert e.value.code == -5
+
+
+def test_c_api_conv_mfft(gpu, orc):
+    n, L = 12, 32
+    rng = np.random.default_rng(1)
+    A = rng.integers(-65535, 65536, size=L * n * n).astype(np.int32)
+    B = rng.integers(-65535, 65536, size=L * n * n).astype(np.int32)
+    cw, err = gpu.conv_mfft(A, B, n, L, gpu.plan(L))
+    assert err == 0
+    assert np.array_equal(cw, orc.conv_limbplane(A, B, n, L))
+
+
+# ---- exact track -------------------------------------------------------------------
+@pytest.mark.parametrize("case", range(13))
+def test_products_fixture(gpu, orc, case):
+    with open(os.path.join(GOLD, "products.json")) as f:
+        c = json.load(f)[case]
+    n, L, RL = c["n"], c["L"], c["RL"]
+    A = orc.bigmat_rand(n, L, c["seed_a"])
+    B = orc.bigmat_rand(n, L, c["seed_b"])
+    with gpu.Ctx(n, L) as ctx:
+        got = ctx.mm(A, B, RL, signed=c["signed"])
+    assert np.array_equal(got, np.array(c["out"], dtype=np.uint16))
+
+
+@pytest.mark.parametrize("n,L", [(8, 32), (48, 32), (24, 128), (10, 64), (7, 16)])
+def test_signed_entries(gpu, orc, n, L):
+    """Two's complement W-bit entries (top limb int16)."""
+    A, A32 = signed_limbs(orc, n, L, SEED + 7)
+    B, B32 = signed_limbs(orc, n, L, SEED_B + 7)
+    RL = 2 * L + 1
+    want = orc.normalize(orc.conv_limbplane(A32, B32, n, L), 2 * L - 1, n, RL)
+    with gpu.Ctx(n, L) as ctx:
+        got = ctx.mm(A, B, RL, signed=True)
+    assert np.array_equal(got, want)
+    out, err = gpu.mm_mfft(A, B, n, L, gpu.plan(L), signed=True)
+    assert err == 0 and np.array_equal(out, want)
+
+
+@pytest.mark.parametrize("RL", [1, 5, 64, 129])
+def test_short_and_long_outputs(gpu, orc, RL):
+    """RL below 2L+1 truncates mod 2^(16 RL), above it zero-extends
+    (src/bigmat.c:48-60)."""
+    n, L = 16, 64
+    A = orc.bigmat_rand(n, L, 3)
+    B = orc.bigmat_rand(n, L, 4)
+    want = orc.normalize(orc.conv_limbplane(A.astype(np.int32), B.astype(np.int32), n, L),
+                         2 * L - 1, n, RL)
+    with gpu.Ctx(n, L) as ctx:
+        assert np.array_equal(ctx.mm(A, B, RL), want)
+
+
+def test_all_ones_worst_case(gpu, orc):
+    """Every limb 0xFFFF: largest transformed values, longest carries."""
+    for n, L in [(64, 128), (16, 64), (32, 32)]:
+        A = np.full(L * n * n, 0xFFFF, np.uint16)
+        RL = 2 * L + 1
+        want = orc.mm_limbplane(A, A, n, L, RL)
+        with gpu.Ctx(n, L) as ctx:
+            assert np.array_equal(ctx.mm(A, A, RL), want), (n, L)
+
+
+def test_generic_kernels_match(gpu, orc, monkeypatch):
+    """The runtime-plan (generic) kernels, forced, give the same bits."""
+    monkeypatch.setenv("MFH_GENERIC_KERNELS", "1")
+    for n, L in [(64, 128), (40, 64), (96, 32)]:
+        A = orc.bigmat_rand(n, L, SEED)
+        B = orc.bigmat_rand(n, L, SEED_B)
+        RL = 2 * L + 1
+        want = orc.mm_mfft(A, B, n, L, orc.plan(L), RL)
+        with gpu.Ctx(n, L) as ctx:
+            assert np.array_equal(ctx.mm(A, B, RL), want), (n, L)
+
+
+def test_device_generator_matches_host(gpu, orc, lib):
+    n, L = 96, 32
+    with gpu.Ctx(n, L) as ctx:
+        d = gpu.DevBuf(L * n * n * 2)
+        gpu.check(lib.mfh_rand_u16_dev(ctx.h, d.ptr, n, L, SEED))
+        ctx.sync()
+        got = d.download(np.uint16, L * n * n)
+        d.free()
+    assert np.array_equal(got, orc.bigmat_rand(n, L, SEED))
+    x = gpu.DevBuf(4 * 1000)
+    gpu.check(lib.mfh_rand_f32_dev(None, x.ptr, 1000, 77, -20, 20))
+    gpu.check(lib.mfh_sync(None))
+    assert np.array_equal(x.download(np.float32, 1000), orc.fp32_rand(1000, 77, -20, 20))
+    x.free()
+
+
+def test_device_normalize(gpu, orc):
+    with open(os.path.join(GOLD, "normalize.json")) as f:
+        for c in json.load(f):
+            acc = np.array(c["acc"], dtype=np.int64)
+            out, err = gpu.normalize_planes(acc, c["nplanes"], c["n"], c["RL"])
+            assert err == 0
+            assert np.array_equal(out, np.array(c["out"], dtype=np.uint16))
+
+
+# ---- fp32 embedding -------------------------------------------------------------------
+@pytest.mark.parametrize("case", range(3))
+def test_fpx_fixture(gpu, orc, lib, case):
+    with open(os.path.join(GOLD, "fpx.json")) as f:
+        c = json.load(f)[case]
+    n = c["n"]
+    A = np.array(c["A_bits"], dtype=np.uint32).view(np.float32)
+    B = np.array(c["B_bits"], dtype=np.uint32).view(np.float32)
+    want = np.array(c["C_bits"], dtype=np.uint32)
+    ctx = gpu.FpxCtx()
+    assert lib.fpx_init(C.byref(ctx), A.ctypes.data, B.ctypes.data, n, 512) == 0
+    lib.fpx_encode(C.byref(ctx), A.ctypes.data, B.ctypes.data)
+    assert lib.mfft_last_error() == 0
+    out = np.empty(n * n, np.float32)
+    assert lib.fpx_mm_f32(C.byref(ctx), C.byref(gpu.plan(ctx.L)), out.ctypes.data) == 0
+    assert np.array_equal(out.view(np.uint32), want)
+    # reference-style call sequence: encode -> conv_mfft -> decode
+    nn = n * n
+    cw = np.ctypeslib.as_array(C.cast(ctx.Cw, C.POINTER(C.c_int64)), shape=((2 * ctx.L - 1) * nn,))
+    a32 = np.ctypeslib.as_array(C.cast(ctx.A32, C.POINTER(C.c_int32)), shape=(ctx.L * nn,))
+    b32 = np.ctypeslib.as_array(C.cast(ctx.B32, C.POINTER(C.c_int32)), shape=(ctx.L * nn,))
+    oc = orc.fpx(A, B, n, 512)
+    oa, ob = orc.fpx_planes(oc)
+    orc.fpx_free(oc)
+    assert np.array_equal(a32, oa) and np.array_equal(b32, ob)   # device encode
+    lib.conv_mfft(ctx.Cw, ctx.A32, ctx.B32, n, ctx.L, C.byref(gpu.plan(ctx.L)), gpu.KERNEL_HIP)
+    assert lib.mfft_last_error() == 0
+    assert np.array_equal(cw, orc.conv_limbplane(oa, ob, n, ctx.L))
+    out2 = np.empty(n * n, np.float32)
+    lib.fpx_decode_f32(C.byref(ctx), out2.ctypes.data)
+    assert np.array_equal(out2.view(np.uint32), want)
+    lib.fpx_free(C.byref(ctx))
+
+
+def test_fpx_zero_and_signs(gpu, orc, lib):
+    n = 64
+    A = orc.fp32_rand(n * n, 9, -20, 20)
+    B = orc.fp32_rand(n * n, 10, -20, 20)
+    A[: n] = 0.0                                          # row 0 of C is exactly zero
+    with gpu.Ctx(n, 32) as ctx:
+        got = ctx.fpx_mm(A, B, 256, 256)
+    oc = orc.fpx(A, B, n, 512)
+    oa, ob = orc.fpx_planes(oc)
+    want = orc.fpx_decode_from(oc, orc.conv_limbplane(oa, ob, n, 32))
+    orc.fpx_free(oc)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.all(got[:n].view(np.uint32) == 0)           # +0.0f
+
+
+# ---- full-size workloads ------------------------------------------------------------------
+def check_large(gpu, orc, lib, n, W, signed):
+    L = W // 16
+    RL = 2 * L + 1
+    print(f"[large] n={n} W={W} signed={signed}", flush=True)
+    with gpu.Ctx(n, L) as ctx:
+        dA, dB, dO = gpu.DevBuf(L * n * n * 2), gpu.DevBuf(L * n * n * 2), gpu.DevBuf(RL * n * n * 2)
+        gpu.check(lib.mfh_rand_u16_dev(ctx.h, dA.ptr, n, L, SEED))
+        gpu.check(lib.mfh_rand_u16_dev(ctx.h, dB.ptr, n, L, SEED_B))
+        kind = gpu.MFH_IN_U16_SIGNED if signed else gpu.MFH_IN_U16
+        gpu.check(lib.mfh_mm_dev(ctx.h, kind, dA.ptr, dB.ptr, dO.ptr, RL))
+        ctx.sync()
+        out = dO.download(np.uint16, RL * n * n)
+        for b in (dA, dB, dO):
+            b.free()
+    A = orc.bigmat_rand(n, L, SEED)
+    B = orc.bigmat_rand(n, L, SEED_B)
+    assert orc.freivalds(A, B, n, L, out, RL, signed_top=signed, nprimes=2)
+    rng = np.random.default_rng(n + W)
+    picks = [(0, 0), (n - 1, n - 1)] + [tuple(int(v) for v in rng.integers(0, n, 2)) for _ in range(6)]
+    for i, j in picks:
+        want = orc.entry_exact(A, B, n, L, i, j, RL, signed_top=signed)
+        assert np.array_equal(out.reshape(RL, n * n)[:, i * n + j], want), (i, j)
+
+
+def test_c1_full_against_reference_path(gpu, orc):
+    n, L = 64, 64
+    A = orc.bigmat_rand(n, L, SEED)
+    B = orc.bigmat_rand(n, L, SEED_B)
+    want = orc.mm_mfft(A, B, n, L, orc.plan(L), 2 * L + 1)
+    out, err = gpu.mm_mfft(A, B, n, L, gpu.plan(L))
+    assert err == 0 and np.array_equal(out, want)
+
+
+def test_c3_n1024_w2048(gpu, orc, lib):
+    check_large(gpu, orc, lib, 1024, 2048, False)
+
+
+def test_c2_n256_w8192(gpu, orc, lib):
+    check_large(gpu, orc, lib, 256, 8192, False)
+
+
+def test_c5_n4096_w512_signed(gpu, orc, lib):
+    check_large(gpu, orc, lib, 4096, 512, True)
+
+
+def test_c4_fp32_n2048(gpu, orc):
+    n = 2048
+    A = orc.fp32_rand(n * n, SEED, -20, 20)
+    B = orc.fp32_rand(n * n, SEED_B, -20, 20)
+    with gpu.Ctx(n, 32) as ctx:
+        got = ctx.fpx_mm(A, B, 256, 256)
+        cw_dev = None
+    oc = orc.fpx(A, B, n, 512)
+    oa, ob = orc.fpx_planes(oc)
+    # the exact product's planes from the GPU's own conv path, checked by
+    # Freivalds, then decoded by the oracle and compared bit for bit
+    with gpu.Ctx(n, 32) as ctx:
+        cw_dev = ctx.conv(oa, ob)
+    assert orc.freivalds_conv(oa, ob, n, 32, cw_dev, nprimes=2)
+    want = orc.fpx_decode_from(oc, cw_dev)
+    orc.fpx_free(oc)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
