@@ -27,45 +27,104 @@ INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
 HBM_PEAK_GBS = 8000.0
 
 CONFIGS = {
-    # name: (n, W bits, signed)
-    "c1": (64, 1024, False),
-    "c2": (256, 8192, False),
-    "c3": (1024, 2048, False),
-    "c5": (4096, 512, True),
+    # name: (n, W bits, kind)
+    "c1": (64, 1024, "unsigned"),
+    "c2": (256, 8192, "unsigned"),
+    "c3": (1024, 2048, "unsigned"),
+    "c4": (2048, 512, "fp32"),       # fp32 entries on a shared 512-bit grid
+    "c5": (4096, 512, "signed"),
 }
+
+# Freivalds primes below 2^24: residues times residues summed over n <= 4096
+# terms stay below 2^63, so plain int64 numpy suffices
+FREIVALDS_PRIMES = (16777213, 16777199)
+
+
+def planes_mod(planes, n, nlimbs, p, twos):
+    """value of every entry of a plane-major u16 matrix mod p; twos reads the
+    whole number as two's complement of nlimbs limbs"""
+    import numpy as np
+    v = planes.reshape(nlimbs, n * n)
+    acc = np.zeros(n * n, dtype=np.int64)
+    for w in range(nlimbs - 1, -1, -1):
+        acc = (acc * 65536 + v[w].astype(np.int64)) % p
+    if twos:
+        wrap = pow(2, 16 * nlimbs, p)
+        acc = np.where(v[nlimbs - 1] >= 0x8000, (acc - wrap) % p, acc)
+    return acc.reshape(n, n)
+
+
+def entries_mod_signed_top(planes, n, L, p, signed):
+    """inputs: limbs 0..L-2 unsigned, limb L-1 int16 when signed"""
+    import numpy as np
+    v = planes.reshape(L, n * n)
+    acc = np.zeros(n * n, dtype=np.int64)
+    for u in range(L - 1, -1, -1):
+        limb = v[u].astype(np.int64)
+        if signed and u == L - 1:
+            limb = np.where(limb >= 0x8000, limb - 65536, limb)
+        acc = (acc * 65536 + limb) % p
+    return acc.reshape(n, n)
+
+
+def freivalds_check(A, B, out, n, L, RL, signed, seed=7):
+    """out == A*B over Z_p for the primes above and a seeded random vector"""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    for p in FREIVALDS_PRIMES:
+        Am = entries_mod_signed_top(A, n, L, p, signed)
+        Bm = entries_mod_signed_top(B, n, L, p, signed)
+        Cm = planes_mod(out, n, RL, p, signed)
+        r = rng.integers(0, p, size=n, dtype=np.int64)
+        y = (Bm @ r) % p
+        if not np.array_equal((Am @ y) % p, (Cm @ r) % p):
+            return False
+    return True
+
+
+def host_rand_u16(n, L, seed):
+    """SplitMix64 limbs, plane-major (the reference's bigmat_rand), numpy"""
+    import numpy as np
+    i = np.arange(1, L * n * n + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + i * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    return (z & np.uint64(0xFFFF)).astype(np.uint16)
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(n, L, nprod_total, plan_tuple):
+def cpu_baseline(n, L, nprod_total):
     """Reference CPU path (oracle/_ref: the reference's own C sources,
     packed leaf) on a bounded sample, 1 thread.  Pointwise: `s` of the
     NB*K^2 leaf products timed at full n and scaled.  Transform, pack, fold
     and normalize: the reference's own phase profile of a whole mm_mfft at
     n/8 with the same plan, scaled by 64 (those phases are O(n^2))."""
-    from oracle_ctypes import load_reference, Oracle, RefPlanStruct
+    from oracle_ctypes import load_reference
     import numpy as np
     ref = load_reference()
     kind = "reference"
     if ref is None:
         return None
     lib = ref.lib
-    s = 6
     A = np.random.default_rng(1).integers(0, 1 << 16, size=n * n).astype(np.int32)
     B = np.random.default_rng(2).integers(0, 1 << 16, size=n * n).astype(np.int32)
-    # transformed values at the C3 plan are ~21-bit; the leaf's cost does not
-    # depend on the values
+    # transformed values at these plans are at most ~21 bits; the leaf's cost
+    # does not depend on the values.  Time leaf products until ~10 s of work.
     Cacc = np.zeros(n * n, dtype=np.int64)
-    best = 1e30
-    for _ in range(s):
+    times = []
+    while sum(times) < 10.0 and len(times) < 256:
         t0 = time.perf_counter()
         ref.mm_accum(Cacc, A, B, n, 1, ref.KERNEL_PACKED)
-        best = min(best, time.perf_counter() - t0)
-    t_leaf = best
+        times.append(time.perf_counter() - t0)
+    s = len(times)
+    t_leaf = float(np.median(times))
     # phase profile of a whole mm_mfft at n/8
-    ns = max(8, n // 8)
+    ns = min(256, max(8, n // 8))
     prof_on = C.c_int.in_dll(lib, "g_mfft_profile")
 
     class Prof(C.Structure):
@@ -88,7 +147,7 @@ def cpu_baseline(n, L, nprod_total, plan_tuple):
     return {
         "value": round(total_s * 1e3, 1), "unit": "ms", "cores": 1, "kind": kind,
         "sample": (f"reference src/ built from source, packed leaf, 1 thread: {s} of "
-                   f"{nprod_total} n={n} leaf products timed (best {t_leaf:.3f} s each) "
+                   f"{nprod_total} n={n} leaf products timed (median {t_leaf:.3f} s each) "
                    f"x {nprod_total}; other phases from the reference's own profile of one "
                    f"mm_mfft at n={ns} ({rest_small:.3f} s) x {scale:.0f}; extrapolated"),
     }
@@ -102,6 +161,9 @@ def main():
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run the plain copy kernel over MIB MiB, --steps times (the "
+                         "known-size kernel that HBM byte counters are calibrated against)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="HBM bytes per pointwise launch measured by rocprofv3 --pmc")
     args = ap.parse_args()
@@ -115,21 +177,49 @@ def main():
     import numpy as np
     import mfft_ctypes as M
 
-    n, W, signed = CONFIGS[args.config]
+    if args.copy_probe:
+        lib = M.load()
+        nbytes = args.copy_probe << 20
+        src, dst = M.DevBuf(nbytes), M.DevBuf(nbytes)
+        M.check(lib.mfh_rand_u16_dev(None, src.ptr, 1, nbytes // 2, 1))
+        M.check(lib.mfh_sync(None))
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            M.check(lib.mfh_copy_dev(None, dst.ptr, src.ptr, nbytes), "mfh_copy_dev")
+        M.check(lib.mfh_sync(None))
+        dt = (time.perf_counter() - t0) / args.steps
+        log(f"[bench] copy {args.copy_probe} MiB: {dt * 1e3:.3f} ms, "
+            f"{2 * nbytes / dt / 1e9:.1f} GB/s read+write")
+        src.free()
+        dst.free()
+        return
+
+    n, W, ekind = CONFIGS[args.config]
+    signed = ekind == "signed"
+    fp32 = ekind == "fp32"
     L = W // 16
     RL = 2 * L + 1
     lib = M.load()
     p = M.plan(L)
     ctx = M.Ctx(n, L, p)
-    in_bytes = L * n * n * 2
-    dA, dB, dO = M.DevBuf(in_bytes), M.DevBuf(in_bytes), M.DevBuf(RL * n * n * 2)
-    M.check(lib.mfh_rand_u16_dev(ctx.h, dA.ptr, n, L, 12345))
-    M.check(lib.mfh_rand_u16_dev(ctx.h, dB.ptr, n, L, 12345 ^ 0xABCDEF))
+    SA = SB = W // 2
+    if fp32:
+        dA, dB, dO = M.DevBuf(n * n * 4), M.DevBuf(n * n * 4), M.DevBuf(n * n * 4)
+        M.check(lib.mfh_rand_f32_dev(ctx.h, dA.ptr, n * n, 12345, -20, 20))
+        M.check(lib.mfh_rand_f32_dev(ctx.h, dB.ptr, n * n, 12345 ^ 0xABCDEF, -20, 20))
+    else:
+        in_bytes = L * n * n * 2
+        dA, dB, dO = M.DevBuf(in_bytes), M.DevBuf(in_bytes), M.DevBuf(RL * n * n * 2)
+        M.check(lib.mfh_rand_u16_dev(ctx.h, dA.ptr, n, L, 12345))
+        M.check(lib.mfh_rand_u16_dev(ctx.h, dB.ptr, n, L, 12345 ^ 0xABCDEF))
     kind = M.MFH_IN_U16_SIGNED if signed else M.MFH_IN_U16
     ctx.sync()
 
     def step():
-        M.check(lib.mfh_mm_dev(ctx.h, kind, dA.ptr, dB.ptr, dO.ptr, RL), "mfh_mm_dev")
+        if fp32:
+            M.check(lib.mfh_fpx_mm_dev(ctx.h, dA.ptr, dB.ptr, SA, SB, dO.ptr), "mfh_fpx_mm_dev")
+        else:
+            M.check(lib.mfh_mm_dev(ctx.h, kind, dA.ptr, dB.ptr, dO.ptr, RL), "mfh_mm_dev")
 
     log(f"[bench] {args.config}: n={n} W={W} L={L} plan={p} warmup={args.warmup} steps={args.steps}")
     for _ in range(args.warmup):
@@ -157,22 +247,12 @@ def main():
         f"inv {st[2]:.3f} carry {st[3]:.3f}  pointwise {tops_pw:.1f} TOPS")
 
     verified = None
-    if not args.no_verify:
-        from oracle_ctypes import Oracle
-        orc = Oracle()
-        A = orc.bigmat_rand(n, L, 12345)
-        B = orc.bigmat_rand(n, L, 12345 ^ 0xABCDEF)
+    if not args.no_verify and not fp32:
+        A = host_rand_u16(n, L, 12345)
+        B = host_rand_u16(n, L, 12345 ^ 0xABCDEF)
         out = dO.download(np.uint16, RL * n * n)
-        verified = orc.freivalds(A, B, n, L, out, RL, signed_top=signed, nprimes=2)
-        ok_entries = True
-        rng = np.random.default_rng(5)
-        for _ in range(4):
-            i, j = (int(x) for x in rng.integers(0, n, size=2))
-            want = orc.entry_exact(A, B, n, L, i, j, RL, signed_top=signed)
-            got = out.reshape(RL, n * n)[:, i * n + j]
-            ok_entries &= bool(np.array_equal(want, got))
-        verified = bool(verified and ok_entries)
-        log(f"[bench] verification (Freivalds mod 2 primes + 4 exact entries): {verified}")
+        verified = freivalds_check(A, B, out, n, L, RL, signed)
+        log(f"[bench] verification (Freivalds mod 2 primes): {verified}")
 
     traffic = None
     try:
@@ -185,7 +265,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the reference CPU path on a bounded sample ...")
-        cpu = cpu_baseline(n, L, nprod, p)
+        cpu = cpu_baseline(n, L, nprod)
 
     line = {
         "metric": METRIC,
@@ -198,11 +278,14 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": "int8 MFMA, int32/int64 accumulate",
         "data": "synthetic",
-        "config": {"workload": f"exact MFFT matmul, n={n}, W={W}-bit "
-                               f"{'signed' if signed else 'unsigned'} entries (L={L} limbs), "
-                               f"plan S={p.S} NB={p.NB} K={p.K}, seeds 12345/12345^0xABCDEF",
+        "config": {"workload": (f"fp32 embedding on a {W}-bit grid, n={n}, entries +-m*2^e "
+                                 f"(e in [-20, 20]), exact MFFT product rounded once to fp32"
+                                 if fp32 else
+                                 f"exact MFFT matmul, n={n}, W={W}-bit {ekind} entries "
+                                 f"(L={L} limbs)") +
+                               f", plan S={p.S} NB={p.NB} K={p.K}, seeds 12345/12345^0xABCDEF",
                    "n": n, "width_bits": W, "limbs": L, "S": p.S, "NB": p.NB, "K": p.K,
                    "parallelism": "single GPU"},
         "int8_tops_effective": round(tops_issued, 1),

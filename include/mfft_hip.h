@@ -111,6 +111,12 @@ int  mfh_rand_u16_dev(mfh_ctx *ctx, void *dM, int n, int L, uint64_t seed);
 int  mfh_rand_f32_dev(mfh_ctx *ctx, void *dX, size_t count, uint64_t seed,
                       int emin, int emax);
 
+/* Device-to-device copy by a plain streaming kernel (k_copy16), each byte
+ * read once and written once; bytes and both pointers must be multiples of
+ * 16.  No reference counterpart: it is the known-size kernel against which
+ * hardware HBM byte counters are calibrated. */
+int  mfh_copy_dev(mfh_ctx *ctx, void *dst, const void *src, size_t bytes);
+
 /* Per-stage device times (ms) of the most recent product on this context,
  * measured with HIP events on the context's stream:
  *   [0] transforms in (both operands), [1] pointwise GEMM,

@@ -102,6 +102,7 @@ int mfh_launch_encode_f32(const float *X, int n, int L, int S, int32_t *out,
                           hipStream_t st);
 int mfh_launch_decode_f32(mfh_ctx *c, const int64_t *Cw, int SAB, float *out);
 int mfh_launch_rand_u16(void *dst, size_t count, uint64_t seed, hipStream_t st);
+int mfh_launch_copy16(void *dst, const void *src, size_t bytes, hipStream_t st);
 int mfh_launch_rand_f32(void *dst, size_t count, uint64_t seed, int emin,
                         int emax, hipStream_t st);
 

@@ -345,6 +345,14 @@ int mfh_rand_f32_dev(mfh_ctx *c, void *dX, size_t count, uint64_t seed, int emin
     return mfh_launch_rand_f32(dX, count, seed, emin, emax, c ? c->stream : 0);
 }
 
+int mfh_copy_dev(mfh_ctx *c, void *dst, const void *src, size_t bytes)
+{
+    if (!dst || !src || bytes % 16 || ((uintptr_t)dst | (uintptr_t)src) % 16)
+        return MFH_E_ARG;
+    if (!bytes) return MFH_OK;
+    return mfh_launch_copy16(dst, src, bytes, c ? c->stream : 0);
+}
+
 int mfh_set_timing(mfh_ctx *c, int enable)
 {
     if (!c) return MFH_E_ARG;

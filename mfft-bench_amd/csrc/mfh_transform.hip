@@ -688,6 +688,16 @@ __global__ __launch_bounds__(256) void k_rand_f32(float *dst, size_t count,
     }
 }
 
+// plain 16-byte-vector copy: reads and writes each byte once, the yardstick
+// that HBM byte counters are calibrated against
+__global__ __launch_bounds__(256) void k_copy16(const uint4 *__restrict__ src,
+                                                uint4 *__restrict__ dst, size_t count)
+{
+    size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * 256;
+    for (; idx < count; idx += stride) dst[idx] = src[idx];
+}
+
 int lg2i(int x) { int r = 0; while ((1 << r) < x) ++r; return r; }
 
 unsigned grid_for(size_t count, unsigned cap)
@@ -907,6 +917,15 @@ int mfh_launch_rand_u16(void *dst, size_t count, uint64_t seed, hipStream_t st)
 {
     hipLaunchKernelGGL(k_rand_u16, dim3(grid_for(count, 65536)), dim3(256), 0, st,
                        (uint16_t *)dst, count, seed);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_copy16(void *dst, const void *src, size_t bytes, hipStream_t st)
+{
+    const size_t count = bytes / 16;
+    hipLaunchKernelGGL(k_copy16, dim3(grid_for(count, 8192)), dim3(256), 0, st,
+                       (const uint4 *)src, (uint4 *)dst, count);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }

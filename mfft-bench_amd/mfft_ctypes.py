@@ -74,6 +74,7 @@ def load(path=None):
         "mfh_h2d": ([vp, vp, sz], i), "mfh_d2h": ([vp, vp, sz], i), "mfh_sync": ([vp], i),
         "mfh_rand_u16_dev": ([vp, vp, i, i, u64], i),
         "mfh_rand_f32_dev": ([vp, vp, sz, u64, i, i], i),
+        "mfh_copy_dev": ([vp, vp, vp, sz], i),
         "mfh_set_timing": ([vp, i], i), "mfh_stage_times": ([vp, C.POINTER(C.c_float)], i),
         "mfh_work": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double)], i),
         "mfft_plan_init": ([pl, i, i], i), "mfft_plan_products": ([pl], C.c_longlong),

@@ -138,6 +138,20 @@ def test_device_generator_matches_host(gpu, orc, lib):
     x.free()
 
 
+@pytest.mark.gpu
+def test_copy_kernel(gpu, lib):
+    nbytes = 3 * (1 << 20) + 4096
+    src, dst = gpu.DevBuf(nbytes), gpu.DevBuf(nbytes)
+    data = np.random.default_rng(3).integers(0, 256, nbytes, dtype=np.uint8)
+    src.upload(data)
+    gpu.check(lib.mfh_copy_dev(None, dst.ptr, src.ptr, nbytes))
+    gpu.check(lib.mfh_sync(None))
+    assert np.array_equal(dst.download(np.uint8, nbytes), data)
+    assert lib.mfh_copy_dev(None, dst.ptr, src.ptr, nbytes - 8) == -3   # not a multiple of 16
+    src.free()
+    dst.free()
+
+
 def test_device_normalize(gpu, orc):
     with open(os.path.join(GOLD, "normalize.json")) as f:
         for c in json.load(f):
