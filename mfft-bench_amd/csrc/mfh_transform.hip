@@ -179,12 +179,12 @@ struct LimbsI32 {
     __device__ __forceinline__ int get(int u) const { return r[u]; }
 };
 
-// Packed limb pairs staged in LDS for the whole workgroup: pair p of
-// element slot t at lds[p * 256 + t] (consecutive threads read consecutive
+// Packed limb pairs staged in LDS for the E elements of a workgroup: pair p
+// of element slot t at lds[p * E + t] (consecutive threads read consecutive
 // dwords: conflict-free).  Filled with 16-byte loads of 8 consecutive
 // elements of planes 2p and 2p+1 (the input row length must be a multiple
 // of 8, so such a run never straddles a row end).
-template <int L>
+template <int L, int E = 256>
 struct LimbsLds {
     const uint32_t *base;      // lds + thread slot
     bool top_signed;
@@ -193,20 +193,20 @@ struct LimbsLds {
     __device__ __forceinline__ int get(int u) const
     {
         if (recoded && u == L - 1) return top;
-        const uint32_t w = base[(u / 2) * 256];
+        const uint32_t w = base[(u / 2) * E];
         if (recoded) return (u & 1) ? (int)(short)(w >> 16) : (int)(short)(w & 0xFFFFu);
         if (u == L - 1 && top_signed) return (int)(short)(w >> 16);
         return (u & 1) ? (int)(w >> 16) : (int)(w & 0xFFFFu);
     }
 };
 
-template <int L>
+template <int L, int E>
 __device__ __forceinline__ void stage_limbs_u16(uint32_t *lds, const uint16_t *src, int n,
                                                 size_t nn, int np_, size_t e0)
 {
-    constexpr int NP2 = L / 2;
-    for (int t = threadIdx.x; t < NP2 * 32; t += 256) {
-        const int p = t >> 5, g8 = t & 31;
+    constexpr int NP2 = L / 2, R8 = E / 8;      // 8-element runs per plane pair
+    for (int t = threadIdx.x; t < NP2 * R8; t += 256) {
+        const int p = t / R8, g8 = t % R8;
         const size_t e = e0 + 8 * g8;
         const int i = (int)(e / np_), k = (int)(e % np_);
         uint4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
@@ -221,7 +221,7 @@ __device__ __forceinline__ void stage_limbs_u16(uint32_t *lds, const uint16_t *s
             w[2 * d] = __builtin_amdgcn_perm(h4[d], l4[d], 0x05040100u);     // lo16(l)|lo16(h)<<16
             w[2 * d + 1] = __builtin_amdgcn_perm(h4[d], l4[d], 0x07060302u); // hi16(l)|hi16(h)<<16
         }
-        uint4 *dst = (uint4 *)(lds + p * 256 + 8 * g8);
+        uint4 *dst = (uint4 *)(lds + p * E + 8 * g8);
         dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
         dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
     }
@@ -308,27 +308,46 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
     }
 }
 
-template <int S, int NB, int Q, int MODE, class Limbs, int... qs>
-__device__ __forceinline__ void forward_classes(const Limbs &x, int8_t *o, size_t nnp,
-                                                std::integer_sequence<int, qs...>)
+// Threads of part p (p = thread / E, wave-uniform) produce the output
+// classes q = p, p + TPE, ... of their element.
+template <int S, int NB, int Q, int MODE, int TPE, int PART, class Limbs, int... is>
+__device__ __forceinline__ void forward_part(const Limbs &x, int8_t *o, size_t nnp,
+                                             std::integer_sequence<int, is...>)
 {
-    (forward_class<S, NB, Q, qs, MODE, Limbs>(x, o, nnp), ...);
+    (forward_class<S, NB, Q, PART + TPE * is, MODE, Limbs>(x, o, nnp), ...);
+}
+template <int S, int NB, int Q, int MODE, int TPE, class Limbs, int PART = 0>
+__device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *o, size_t nnp)
+{
+    if constexpr (PART < TPE) {
+        if (part == PART)
+            forward_part<S, NB, Q, MODE, TPE, PART, Limbs>(x, o, nnp,
+                                                           std::make_integer_sequence<int, Q / TPE>{});
+        else
+            forward_parts<S, NB, Q, MODE, TPE, Limbs, PART + 1>(part, x, o, nnp);
+    }
 }
 
-template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src>
+// E elements per workgroup of 256 threads, 256/E threads per element.
+template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src, int E = 256>
 __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restrict__ out, int np_,
                                                       int top_signed)
 {
     constexpr int L = NB * S / 2;
+    constexpr int TPE = 256 / E;
+    static_assert(E * TPE == 256 && Q % TPE == 0, "threads split evenly over classes");
+    static_assert(!RECODE || TPE == 1, "recoding rewrites the staged limbs in place");
     const size_t nnp = (size_t)np_ * np_;
-    const size_t e0 = (size_t)blockIdx.x * 256;
-    const size_t e = e0 + threadIdx.x;
+    const size_t e0 = (size_t)blockIdx.x * E;
+    const int slot = threadIdx.x % E;
+    const int part = __builtin_amdgcn_readfirstlane(threadIdx.x / E);
+    const size_t e = e0 + slot;
     Limbs x;
-    if constexpr (std::is_same_v<Limbs, LimbsLds<L>>) {
-        __shared__ uint32_t stage[(L / 2) * 256];
-        stage_limbs_u16<L>(stage, src.p, src.n, src.nn, np_, e0);
+    if constexpr (std::is_same_v<Limbs, LimbsLds<L, E>>) {
+        __shared__ uint32_t stage[(L / 2) * E];
+        stage_limbs_u16<L, E>(stage, src.p, src.n, src.nn, np_, e0);
         __syncthreads();
-        x.base = stage + threadIdx.x;
+        x.base = stage + slot;
         x.top_signed = top_signed != 0;
         x.recoded = RECODE;
         if constexpr (RECODE) {
@@ -336,11 +355,11 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
             // c_(u+1) = [x_u + c_u >= 2^15]: the same integer, limbs below
             // the top in [-2^15, 2^15), the top limb x + c unrecoded.  This
             // halves the bound on the transformed values.
-            uint32_t *slot = stage + threadIdx.x;
+            uint32_t *sl = stage + slot;
             int carry = 0;
 #pragma unroll 8
             for (int p2 = 0; p2 < L / 2; ++p2) {
-                const uint32_t w = slot[p2 * 256];
+                const uint32_t w = sl[p2 * E];
                 int lo = (int)(w & 0xFFFFu) + carry;
                 carry = lo >= 32768;
                 lo -= carry << 16;
@@ -352,7 +371,7 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
                     x.top = top_signed ? (int)(short)(w >> 16) + carry : hi;
                     hi = 0;
                 }
-                slot[p2 * 256] = ((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16);
+                sl[p2 * E] = ((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16);
             }
         }
         if (e >= nnp) return;
@@ -363,7 +382,7 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
         load_limbs<L>(x, src, i, k, valid);
         if constexpr (std::is_same_v<Limbs, LimbsPacked<L>>) x.top_signed = top_signed != 0;
     }
-    forward_classes<S, NB, Q, MODE, Limbs>(x, out + e, nnp, std::make_integer_sequence<int, Q>{});
+    forward_parts<S, NB, Q, MODE, TPE, Limbs>(part, x, out + e, nnp);
 }
 
 // |limb| <= 65535 for int32 inputs (the transform and digit bounds assume it)
@@ -727,14 +746,15 @@ int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
 }
 
 namespace {
-// compile-time plans: (S, NB) with the class count Q = NB/4
-template <int S, int NB, int MODE, bool RECODE, class Src, class Limbs>
+// compile-time plans: (S, NB) with Q output classes of length NB/Q
+template <int S, int NB, int MODE, bool RECODE, class Src, class Limbs, int E = 256,
+          int Q = NB / 4>
 bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_signed)
 {
     if (c->S != S || c->NB != NB || c->mode != MODE || (c->recode != 0) != RECODE) return false;
     const size_t nnp = (size_t)c->np * c->np;
-    hipLaunchKernelGGL((k_forward_fast<S, NB, NB / 4, MODE, RECODE, Limbs, Src>),
-                       dim3((unsigned)((nnp + 255) / 256)), dim3(256), 0, c->stream, s, dst,
+    hipLaunchKernelGGL((k_forward_fast<S, NB, Q, MODE, RECODE, Limbs, Src, E>),
+                       dim3((unsigned)((nnp + E - 1) / E)), dim3(256), 0, c->stream, s, dst,
                        c->np, top_signed);
     return true;
 }
@@ -746,6 +766,8 @@ bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int top_signed)
     return try_fast<8, 32, K7, true, SrcU16, LimbsLds<128>>(c, s, dst, top_signed) ||  // W=2048
            try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>>(c, s, dst, top_signed) ||
            try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>>(c, s, dst, top_signed) ||  // W=1024
+           try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst,   // W=8192
+                                                                         top_signed) ||
            try_fast<4, 16, K7, false, SrcU16, LimbsPacked<32>>(c, s, dst, top_signed); // W=512
 }
 }  // namespace
@@ -848,7 +870,8 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw)
 {
     if (c->use_fast && (try_inverse_fast<32, 16>(c, Cw) ||   // W=2048
                         try_inverse_fast<16, 16>(c, Cw) ||   // W=1024
-                        try_inverse_fast<16, 8>(c, Cw))) {   // W=512
+                        try_inverse_fast<16, 8>(c, Cw) ||    // W=512
+                        try_inverse_fast<64, 32>(c, Cw))) {  // W=8192
         MFH_HIP(hipGetLastError());
         return MFH_OK;
     }

@@ -13,7 +13,8 @@ SMALL = [(1, 2, 0), (5, 4, 0), (8, 8, 0), (16, 16, 0), (8, 32, 3), (13, 32, 0),
          (8, 64, 0), (7, 128, 0), (3, 256, 0), (6, 512, 0), (64, 64, 0), (70, 32, 0),
          (100, 16, 0),
          # compile-time specialised transforms (n a multiple of 8)
-         (24, 128, 0), (64, 128, 0), (40, 64, 0), (96, 32, 0), (136, 32, 0)]
+         (24, 128, 0), (64, 128, 0), (40, 64, 0), (96, 32, 0), (136, 32, 0), (16, 512, 0),
+         (24, 512, 0)]
 
 
 @pytest.mark.parametrize("n,L,sigma", SMALL)
