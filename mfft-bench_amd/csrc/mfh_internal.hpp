@@ -87,14 +87,16 @@ struct mfh_ctx {
     float stage_ms[5];
 };
 
-// kernel launchers (mfh_kernels.hip)
+// kernel launchers (mfh_transform.hip, mfh_pointwise.hip)
 int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
                          int elem_bytes, hipStream_t st);
 int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
                        int scale_S);
 int mfh_launch_check_i32(mfh_ctx *c, const int32_t *src, int planes);
 int mfh_launch_pointwise(mfh_ctx *c);
-int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw);
+// out != nullptr asks for the carry into RL uint16 limbs to be fused;
+// *carried tells whether it was (else Cw holds the coefficient planes)
+int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carried);
 int mfh_launch_carry(mfh_ctx *c, const int64_t *Cw, uint16_t *out, int RL);
 int mfh_launch_carry_planes(const int64_t *Cw, int P, size_t nn, uint16_t *out,
                             int RL, hipStream_t st);

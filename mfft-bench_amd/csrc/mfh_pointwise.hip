@@ -45,16 +45,20 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int pmod(int a, int m) { return ((a % m) + m) % m; }
 
-template <int K_, int T_, int WBI_, int WBJ_>
+// KB: 64-wide k blocks per LDS fill (1, or 2 for small rings, where one
+// block alone gives too few MFMAs per barrier)
+template <int K_, int T_, int WBI_, int WBJ_, int KB_ = 1>
 struct PwCfg {
-    static constexpr int K = K_, T = T_, WBI = WBI_, WBJ = WBJ_;
+    static constexpr int K = K_, T = T_, WBI = WBI_, WBJ = WBJ_, KB = KB_;
+    static_assert(KB == 1 || KB == 2, "one or two k blocks per fill");
     static constexpr int G = K / T;                 // t-groups per block
     static constexpr int WAVES = WBI * WBJ * G;
     static constexpr int THREADS = WAVES * 64;
     static constexpr int BI = 16 * WBI, BJ = 16 * WBJ;
     static constexpr int A_CHUNKS = K * WBI * 64;   // 16-byte LDS chunks
     static constexpr int B_CHUNKS = K * WBJ * 64;
-    static constexpr int LDS_BYTES = (A_CHUNKS + B_CHUNKS) * 16;   // one round buffer
+    static constexpr int SUB_CHUNKS = A_CHUNKS + B_CHUNKS;         // one k block
+    static constexpr int LDS_BYTES = KB * SUB_CHUNKS * 16;          // one fill
 };
 
 // One round: one 64-wide k block of one digit pair, all K values of c2.
@@ -267,29 +271,36 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     v4i *wbp = lds + Cfg::A_CHUNKS + wave * 64 + lane;
     const v4i *la = lds + wbi * 64 + lane;
     const v4i *lb = lds + Cfg::A_CHUNKS + wbj * 64 + lane;
-    const int kblocks = np_ / MFH_KBLK;
+    constexpr int KB = Cfg::KB, SUB = Cfg::SUB_CHUNKS, NF = NA + NBF;
+    const int kblocks = np_ / (MFH_KBLK * KB);        // fills per digit pair
     const int col = j0 + wbj * 16 + (lane & 15);
     int32_t *out_base = C5 + (((size_t)jp * np_ + i0 + wbi * 16 + 4 * (lane >> 4)) * np_ + col) *
                                  (NCLASS * K) + tg * T;
 
-    v4i R[NA + NBF];
+    v4i R[KB * NF];
     auto gload = [&](RoundPos q) {
         int rlo, np2;
         class_pairs<MODE>(q.m, rlo, np2);
         const int r = rlo + q.idx / kblocks, kb = q.idx % kblocks;
         const int s = MODE == MFH_MODE_K7 ? r : q.m - r;
-        const int8_t *a0 = a_blk + (size_t)r * plane + kb * MFH_KBLK;
-        const int8_t *b0 = b_blk + (size_t)s * plane + kb * MFH_KBLK;
 #pragma unroll
-        for (int i = 0; i < NA; ++i) R[i] = *(const v4i *)(a0 + i * da);
+        for (int sb = 0; sb < KB; ++sb) {
+            const int8_t *a0 = a_blk + (size_t)r * plane + (kb * KB + sb) * MFH_KBLK;
+            const int8_t *b0 = b_blk + (size_t)s * plane + (kb * KB + sb) * MFH_KBLK;
 #pragma unroll
-        for (int i = 0; i < NBF; ++i) R[NA + i] = *(const v4i *)(b0 + i * db);
+            for (int i = 0; i < NA; ++i) R[sb * NF + i] = *(const v4i *)(a0 + i * da);
+#pragma unroll
+            for (int i = 0; i < NBF; ++i) R[sb * NF + NA + i] = *(const v4i *)(b0 + i * db);
+        }
     };
     auto lwrite = [&]() {
 #pragma unroll
-        for (int i = 0; i < NA; ++i) wa[i * W * 64] = R[i];
+        for (int sb = 0; sb < KB; ++sb) {
 #pragma unroll
-        for (int i = 0; i < NBF; ++i) wbp[i * W * 64] = R[NA + i];
+            for (int i = 0; i < NA; ++i) wa[sb * SUB + i * W * 64] = R[sb * NF + i];
+#pragma unroll
+            for (int i = 0; i < NBF; ++i) wbp[sb * SUB + i * W * 64] = R[sb * NF + NA + i];
+        }
     };
     auto next_of = [&](RoundPos q) {
         int rlo, np2;
@@ -309,9 +320,16 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     v4i acc[T];
     // one round: MFMAs from LDS, then hand the registers' round to LDS and
     // start loading the one after
+    // with two k blocks per fill the fill runs one ascending and one
+    // descending pass, which leaves the accumulator's orientation unchanged
     auto step = [&](auto asc_tag) {
         constexpr bool ASC = decltype(asc_tag)::value;
-        pw_dispatch<Cfg, ASC>(tg, acc, la, lb, NoIssue{});
+        if constexpr (KB == 1) {
+            pw_dispatch<Cfg, ASC>(tg, acc, la, lb, NoIssue{});
+        } else {
+            pw_dispatch<Cfg, true>(tg, acc, la, lb, NoIssue{});
+            pw_dispatch<Cfg, false>(tg, acc, la + SUB, lb + SUB, NoIssue{});
+        }
         __syncthreads();                     // every wave is done reading LDS
         cur = nxt;
         if (cur.m < NCLASS) {
@@ -329,14 +347,20 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
         class_pairs<MODE>(m, rlo, np2);
         const int rounds = np2 * kblocks;
         int rd = 0;
+        bool flip = false;
+        if constexpr (KB == 1) {
 #pragma unroll 1
-        for (; rd + 1 < rounds; rd += 2) {
-            step(std::true_type{});
-            step(std::false_type{});
+            for (; rd + 1 < rounds; rd += 2) {
+                step(std::true_type{});
+                step(std::false_type{});
+            }
+            // after an ascending round the accumulator holds -(P-N)
+            flip = rd < rounds;
+            if (flip) step(std::true_type{});
+        } else {
+#pragma unroll 1
+            for (; rd < rounds; ++rd) step(std::true_type{});
         }
-        // after an ascending round the accumulator holds -(P-N)
-        const bool flip = rd < rounds;
-        if (flip) step(std::true_type{});
         // store this class: rows 4*(lane/16)+v, column lane%16, T values of t
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -357,6 +381,7 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
 template <class Cfg>
 int launch_cfg(mfh_ctx *c)
 {
+    if (c->np % (MFH_KBLK * Cfg::KB)) return MFH_E_UNSUPPORTED;
     const int tiles_i = c->np / Cfg::BI, tiles_j = c->np / Cfg::BJ;
     static bool attr_set = false;
     if (!attr_set) {
@@ -385,7 +410,9 @@ int mfh_launch_pointwise(mfh_ctx *c)
 {
     switch (c->K) {
     case 4:  return launch_cfg<PwCfg<4, 4, 2, 2>>(c);
-    case 8:  return launch_cfg<PwCfg<8, 8, 2, 2>>(c);
+    case 8:
+        return c->np % 128 == 0 ? launch_cfg<PwCfg<8, 8, 2, 2, 2>>(c)
+                                : launch_cfg<PwCfg<8, 8, 2, 2>>(c);
     case 16: return launch_cfg<PwCfg<16, 16, 2, 2>>(c);
     case 32: return launch_cfg<PwCfg<32, 8, 1, 1>>(c);
     default: return MFH_E_UNSUPPORTED;

@@ -86,9 +86,11 @@ void mark(mfh_ctx *c, int k)
     if (c->timing) (void)hipEventRecord(c->ev[k], c->stream);
 }
 
-// transforms in, pointwise, inverse; leaves the coefficient planes in Cw
+// transforms in, pointwise, inverse; leaves the coefficient planes in Cw,
+// or, when out16 is given and the inverse kernel fuses the carry, the RL
+// output limbs in out16 (*carried = 1)
 int run_conv(mfh_ctx *c, int kind, const void *dA, const void *dB, int64_t *Cw,
-             int SA, int SB)
+             int SA, int SB, uint16_t *out16 = nullptr, int RL = 0, int *carried = nullptr)
 {
     int rc;
     mark(c, 0);
@@ -100,7 +102,9 @@ int run_conv(mfh_ctx *c, int kind, const void *dA, const void *dB, int64_t *Cw,
     mark(c, 1);
     if ((rc = mfh_launch_pointwise(c))) return rc;
     mark(c, 2);
-    if ((rc = mfh_launch_inverse(c, Cw))) return rc;
+    int fused = 0;
+    if ((rc = mfh_launch_inverse(c, Cw, out16, RL, &fused))) return rc;
+    if (carried) *carried = fused;
     mark(c, 3);
     return MFH_OK;
 }
@@ -214,9 +218,10 @@ int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut,
     if (!c || !dA || !dB || !dOut || RL < 1) return MFH_E_ARG;
     if (kind != MFH_IN_U16 && kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
     select_mode(c, true);
-    int rc = run_conv(c, kind, dA, dB, c->dCw, 0, 0);
+    int carried = 0;
+    int rc = run_conv(c, kind, dA, dB, c->dCw, 0, 0, (uint16_t *)dOut, RL, &carried);
     if (rc) return rc;
-    if ((rc = mfh_launch_carry(c, c->dCw, (uint16_t *)dOut, RL))) return rc;
+    if (!carried && (rc = mfh_launch_carry(c, c->dCw, (uint16_t *)dOut, RL))) return rc;
     mark(c, 4);
     return MFH_OK;
 }

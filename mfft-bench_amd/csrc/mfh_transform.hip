@@ -476,10 +476,16 @@ __device__ __forceinline__ long long bperm64(long long v, int addr)
     return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
 }
 
-template <int NB, int K>
+//
+// CARRY: instead of writing Cw, one thread per element (all in the first
+// wave, E <= 64) propagates the carries through the element's 2L-1 planes
+// straight from LDS and writes the RL uint16 output limbs (the semantics of
+// k_carry), saving the int64 round trip through HBM.
+template <int NB, int K, bool CARRY>
 __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict__ C5,
-                                                      int64_t *__restrict__ Cw, int n, int np_,
-                                                      int P, int mode, int ncl)
+                                                      int64_t *__restrict__ Cw,
+                                                      uint16_t *__restrict__ out, int RL,
+                                                      int n, int np_, int P, int mode, int ncl)
 {
     constexpr int S = K / 2, g = 2 * K / NB, twoK = 2 * K;
     constexpr int PASS = 256 / K;            // elements per pass
@@ -539,9 +545,21 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
     }
     __syncthreads();
     const int ecount = (int)((nn - e0) < (size_t)E ? (nn - e0) : (size_t)E);
-    for (int idx = tid; idx < P * E; idx += 256) {
-        const int w = idx / E, el = idx % E;
-        if (el < ecount) Cw[(size_t)w * nn + e0 + el] = cwl[idx];
+    if constexpr (CARRY) {
+        static_assert(E <= 64, "carry lanes must form one wave");
+        if (tid < ecount) {
+            int64_t carry = 0;
+            for (int w = 0; w < RL; ++w) {
+                const int64_t v = carry + (w < P ? cwl[(size_t)w * E + tid] : 0);
+                out[(size_t)w * nn + e0 + tid] = (uint16_t)(v & 0xFFFF);
+                carry = v >> 16;
+            }
+        }
+    } else {
+        for (int idx = tid; idx < P * E; idx += 256) {
+            const int w = idx / E, el = idx % E;
+            if (el < ecount) Cw[(size_t)w * nn + e0 + el] = cwl[idx];
+        }
     }
 }
 
@@ -842,36 +860,50 @@ int mfh_launch_check_i32(mfh_ctx *c, const int32_t *src, int planes)
 }
 
 namespace {
-template <int NB, int K>
-bool try_inverse_fast(mfh_ctx *c, int64_t *Cw)
+template <int NB, int K, bool CARRY>
+bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL)
 {
-    if (c->NB != NB || c->K != K) return false;
     constexpr int E = 2 * (256 / K);
     const int P = 2 * c->L - 1;
     const size_t lds = (size_t)P * E * sizeof(int64_t);
     if (lds > 160 * 1024) return false;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)k_inverse_fast<NB, K>,
+        if (hipFuncSetAttribute((const void *)k_inverse_fast<NB, K, CARRY>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 160 * 1024) != hipSuccess)
             return false;
         attr_set = true;
     }
     const size_t nn = (size_t)c->n * c->n;
-    hipLaunchKernelGGL((k_inverse_fast<NB, K>), dim3((unsigned)((nn + E - 1) / E)), dim3(256),
-                       lds, c->stream, c->dC5, Cw, c->n, c->np, P, c->mode,
+    hipLaunchKernelGGL((k_inverse_fast<NB, K, CARRY>), dim3((unsigned)((nn + E - 1) / E)),
+                       dim3(256), lds, c->stream, c->dC5, Cw, out, RL, c->n, c->np, P, c->mode,
                        mfh_nclasses(c->mode));
     return true;
 }
+// out != nullptr: fused carry into RL uint16 limbs (Cw is not written), for
+// plans with at least 32 elements per workgroup (with fewer, the serial
+// carry lanes cost more than the int64 round trip saves)
+template <int NB, int K>
+bool try_inverse_fast(mfh_ctx *c, int64_t *Cw, uint16_t *&out, int RL)
+{
+    if (c->NB != NB || c->K != K) return false;
+    if constexpr (2 * (256 / K) >= 32) {
+        if (out) return try_inverse_fast_as<NB, K, true>(c, Cw, out, RL);
+    }
+    out = nullptr;
+    return try_inverse_fast_as<NB, K, false>(c, Cw, out, RL);
+}
 }  // namespace
 
-int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw)
+int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carried)
 {
-    if (c->use_fast && (try_inverse_fast<32, 16>(c, Cw) ||   // W=2048
-                        try_inverse_fast<16, 16>(c, Cw) ||   // W=1024
-                        try_inverse_fast<16, 8>(c, Cw) ||    // W=512
-                        try_inverse_fast<64, 32>(c, Cw))) {  // W=8192
+    *carried = 0;
+    if (c->use_fast && (try_inverse_fast<32, 16>(c, Cw, out, RL) ||   // W=2048
+                        try_inverse_fast<16, 16>(c, Cw, out, RL) ||   // W=1024
+                        try_inverse_fast<16, 8>(c, Cw, out, RL) ||    // W=512
+                        try_inverse_fast<64, 32>(c, Cw, out, RL))) {  // W=8192
+        *carried = out != nullptr;
         MFH_HIP(hipGetLastError());
         return MFH_OK;
     }
