@@ -55,6 +55,24 @@ static inline int mfh_nclasses(int mode) { return mode == MFH_MODE_K7 ? 6 : 5; }
 
 #define MFH_CLASSES (2 * MFH_DIGITS - 1)
 
+// Layout of the pointwise step's int32 class results: for point j, element
+// (i, j'), class m and ring coefficient t = 4q + r, with j' = 16 jb + jl,
+//     C5[j][i][m][jb][q][jl][r]       (q < K/4, r < 4, jl < 16)
+// One wave's store of 4 consecutive t of 16 consecutive j' is then 256
+// contiguous bytes, and the K values of 16 consecutive elements lie in one
+// K*64-byte run.  Index of class 0 of (j, i, j', t); classes are
+// mfh_c5_class_stride(np, K) ints apart.
+__host__ __device__ inline size_t mfh_c5_index(int j, int i, int jj, int t, int np_, int ncl,
+                                               int K)
+{
+    const size_t row = ((size_t)j * np_ + i) * ncl;            // class 0 of (j, i)
+    return ((row * (np_ / 16) + jj / 16) * (K / 4) + t / 4) * 64 + (jj & 15) * 4 + (t & 3);
+}
+__host__ __device__ inline size_t mfh_c5_class_stride(int np_, int K)
+{
+    return (size_t)K * np_;
+}
+
 // class accumulators provably fit int32: a class has at most 3 (B8) or 1
 // (K7) digit products of np/64 rounds, each round at most K * 64 * 2^14
 static inline bool mfh_class_bound_ok(int K, int np_)
@@ -73,7 +91,7 @@ struct mfh_ctx {
     int recode;           // forward transform recodes limbs to signed form
     int k7_ok;            // plan admits MFH_MODE_K7 (workspace sized for it)
     int8_t *dAh, *dBh;    // digit planes [NB][K][planes][np][np]
-    int32_t *dC5;         // pointwise class results [NB][np][np][classes][K]
+    int32_t *dC5;         // pointwise class results (layout: mfh_c5_index)
     int64_t *dCw;         // coefficient planes [2L-1][n][n]
     void *dBt;            // transposed B input, up to L*n*n int32
     int *dFlag;           // device error flags

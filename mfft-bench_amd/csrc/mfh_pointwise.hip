@@ -33,8 +33,9 @@
 // k bytes 16*(l/16) .. +15; A and B use the same k order, so the dot
 // product is the same whatever order the hardware sums in).
 //
-// Output C^[j][i][j'][t] int64: the K ring coefficients of one element are
-// contiguous, which is the order the inverse transform reads.
+// Output: int32 class results in the layout of mfh_c5_index (4 consecutive
+// ring coefficients of 16 consecutive columns are 256 contiguous bytes, so
+// each wave store writes whole cache lines).
 #include <type_traits>
 
 #include "mfh_internal.hpp"
@@ -229,7 +230,7 @@ __device__ __forceinline__ void class_pairs(int m, int &rlo, int &npairs)
 // fragments stream from global memory into VGPRs; after the round they are
 // written to LDS (one 64 KiB buffer per workgroup).
 //
-// Output C5[j][i][j'][m][t] (int32): C^_j[t] = sum_m C5[..][m][t] 2^(8m).
+// Output: class m of (j, i, j', t) at mfh_c5_index + m * mfh_c5_class_stride.
 // Accumulator bound: a class has at most 3 digit pairs x np/64 rounds of at
 // most K * 2^20 each; mfh_create rejects sizes where that reaches 2^31.
 template <class Cfg, int MODE>
@@ -274,8 +275,7 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     constexpr int KB = Cfg::KB, SUB = Cfg::SUB_CHUNKS, NF = NA + NBF;
     const int kblocks = np_ / (MFH_KBLK * KB);        // fills per digit pair
     const int col = j0 + wbj * 16 + (lane & 15);
-    int32_t *out_base = C5 + (((size_t)jp * np_ + i0 + wbi * 16 + 4 * (lane >> 4)) * np_ + col) *
-                                 (NCLASS * K) + tg * T;
+    const int row0 = i0 + wbi * 16 + 4 * (lane >> 4);
 
     v4i R[KB * NF];
     auto gload = [&](RoundPos q) {
@@ -364,7 +364,6 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
         // store this class: rows 4*(lane/16)+v, column lane%16, T values of t
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            int32_t *dst = out_base + (size_t)v * np_ * (NCLASS * K) + m * K;
 #pragma unroll
             for (int tt = 0; tt < T; tt += 4) {
                 int4 q;
@@ -372,7 +371,8 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
                 q.y = flip ? -acc[tt + 1][v] : acc[tt + 1][v];
                 q.z = flip ? -acc[tt + 2][v] : acc[tt + 2][v];
                 q.w = flip ? -acc[tt + 3][v] : acc[tt + 3][v];
-                *(int4 *)(dst + tt) = q;
+                *(int4 *)(C5 + mfh_c5_index(jp, row0 + v, col, tg * T + tt, np_, NCLASS, K) +
+                          (size_t)m * mfh_c5_class_stride(np_, K)) = q;
             }
         }
     }

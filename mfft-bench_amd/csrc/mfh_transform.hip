@@ -75,19 +75,19 @@ struct SrcF32 {
 };
 
 
-// C^ from the pointwise step's int32 class results (stride K between
+// C^ from the pointwise step's int32 class results (`cs` ints between
 // classes): B8 sum_m class_m 2^(8m); K7 the Karatsuba recombination
-__device__ __forceinline__ long long combine_classes(const int32_t *p, int K, int mode)
+__device__ __forceinline__ long long combine_classes(const int32_t *p, size_t cs, int mode)
 {
     if (mode == MFH_MODE_K7) {
-        const long long P0 = p[0], P1 = p[K], P2 = p[2 * K], P3 = p[3 * K], P4 = p[4 * K],
-                        P5 = p[5 * K];
+        const long long P0 = p[0], P1 = p[cs], P2 = p[2 * cs], P3 = p[3 * cs], P4 = p[4 * cs],
+                        P5 = p[5 * cs];
         const long long c1 = P3 - P0 - P1, c2 = P4 - P0 - P2 + P1, c3 = P5 - P1 - P2;
         return P0 + c1 * 128 + c2 * 16384 + c3 * 2097152 + P2 * 268435456;
     }
     long long v = 0;
 #pragma unroll
-    for (int m = MFH_CLASSES - 1; m >= 0; --m) v = v * 256 + (long long)p[m * K];
+    for (int m = MFH_CLASSES - 1; m >= 0; --m) v = v * 256 + (long long)p[m * cs];
     return v;
 }
 
@@ -424,8 +424,8 @@ __global__ void k_inverse_fold(const int32_t *__restrict__ C5,
     if (valid) {
         for (int j = 0; j < NB; ++j) {
             const int r = lgNB ? (int)(__brev((unsigned)j) >> (32 - lgNB)) : 0;
-            X[r * K + c] = combine_classes(C5 + (((size_t)j * np_ + i) * np_ + jj) * (ncl * K) + c,
-                                           K, mode);
+            X[r * K + c] = combine_classes(C5 + mfh_c5_index(j, i, jj, c, np_, ncl, K),
+                                           mfh_c5_class_stride(np_, K), mode);
         }
     }
     __syncthreads();
@@ -510,8 +510,8 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
 #pragma unroll
             for (int bit = 1, rb = NB >> 1; bit < NB; bit <<= 1, rb >>= 1)
                 if (j & bit) r |= rb;
-            X[r] = valid ? combine_classes(C5 + (((size_t)j * np_ + i) * np_ + jj) * (ncl * K) + c,
-                                           K, mode)
+            X[r] = valid ? combine_classes(C5 + mfh_c5_index(j, i, jj, c, np_, ncl, K),
+                                           mfh_c5_class_stride(np_, K), mode)
                          : 0;
         }
 #pragma unroll
