@@ -181,7 +181,7 @@ def main():
         lib = M.load()
         nbytes = args.copy_probe << 20
         src, dst = M.DevBuf(nbytes), M.DevBuf(nbytes)
-        M.check(lib.mfh_rand_u16_dev(None, src.ptr, 1, nbytes // 2, 1))
+        M.check(lib.mfh_rand_u16_dev(None, src.ptr, 1024, nbytes // (2 << 20), 1))
         M.check(lib.mfh_sync(None))
         t0 = time.perf_counter()
         for _ in range(args.steps):

@@ -371,8 +371,11 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
                 q.y = flip ? -acc[tt + 1][v] : acc[tt + 1][v];
                 q.z = flip ? -acc[tt + 2][v] : acc[tt + 2][v];
                 q.w = flip ? -acc[tt + 3][v] : acc[tt + 3][v];
-                *(int4 *)(C5 + mfh_c5_index(jp, row0 + v, col, tg * T + tt, np_, NCLASS, K) +
-                          (size_t)m * mfh_c5_class_stride(np_, K)) = q;
+                // read once, by the inverse transform: stream past the caches
+                const v4i qv = {q.x, q.y, q.z, q.w};
+                __builtin_nontemporal_store(
+                    qv, (v4i *)(C5 + mfh_c5_index(jp, row0 + v, col, tg * T + tt, np_, NCLASS, K) +
+                                (size_t)m * mfh_c5_class_stride(np_, K)));
             }
         }
     }

@@ -80,14 +80,19 @@ struct SrcF32 {
 __device__ __forceinline__ long long combine_classes(const int32_t *p, size_t cs, int mode)
 {
     if (mode == MFH_MODE_K7) {
-        const long long P0 = p[0], P1 = p[cs], P2 = p[2 * cs], P3 = p[3 * cs], P4 = p[4 * cs],
-                        P5 = p[5 * cs];
+        // each class value is read once: stream it past the caches
+        const long long P0 = __builtin_nontemporal_load(p), P1 = __builtin_nontemporal_load(p + cs),
+                        P2 = __builtin_nontemporal_load(p + 2 * cs),
+                        P3 = __builtin_nontemporal_load(p + 3 * cs),
+                        P4 = __builtin_nontemporal_load(p + 4 * cs),
+                        P5 = __builtin_nontemporal_load(p + 5 * cs);
         const long long c1 = P3 - P0 - P1, c2 = P4 - P0 - P2 + P1, c3 = P5 - P1 - P2;
         return P0 + c1 * 128 + c2 * 16384 + c3 * 2097152 + P2 * 268435456;
     }
     long long v = 0;
 #pragma unroll
-    for (int m = MFH_CLASSES - 1; m >= 0; --m) v = v * 256 + (long long)p[m * cs];
+    for (int m = MFH_CLASSES - 1; m >= 0; --m)
+        v = v * 256 + (long long)__builtin_nontemporal_load(p + m * cs);
     return v;
 }
 
@@ -551,7 +556,7 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
             int64_t carry = 0;
             for (int w = 0; w < RL; ++w) {
                 const int64_t v = carry + (w < P ? cwl[(size_t)w * E + tid] : 0);
-                out[(size_t)w * nn + e0 + tid] = (uint16_t)(v & 0xFFFF);
+                __builtin_nontemporal_store((uint16_t)(v & 0xFFFF), out + (size_t)w * nn + e0 + tid);
                 carry = v >> 16;
             }
         }
