@@ -197,6 +197,32 @@ __device__ __forceinline__ void pw_load_round(v4i *buf, const int8_t *a0, const 
                                          0, 0);
 }
 
+// Workgroup -> (row tile, column tile, point).  Workgroup w runs on XCD
+// w mod 8, and about 512 consecutive workgroups are resident at once (two
+// per CU).  When the tile grid allows, each such group of 512 covers a
+// 16 x 32 block of tiles of one point and the 64 workgroups of one XCD an
+// 8 x 8 sub-block of it, so that the operand tiles one XCD streams are
+// shared by 8 of its workgroups; otherwise tiles are taken in row order.
+__device__ __forceinline__ void tile_of(int tiles_j, int &ti, int &tj, int &jp)
+{
+    const int per_point = gridDim.x, tiles_i = per_point / tiles_j;
+    if (tiles_i % 16 == 0 && tiles_j % 32 == 0) {
+        const int w = blockIdx.y * per_point + blockIdx.x;
+        const int x = w & 7, q = w >> 3;
+        const int g = q >> 6, ql = q & 63;            // group of 512, slot within XCD
+        const int gpr = tiles_j / 32;                 // groups per 16-row band
+        const int gpp = (tiles_i / 16) * gpr;         // groups per point
+        jp = g / gpp;
+        const int gp = g % gpp;
+        ti = (gp / gpr) * 16 + (x >> 2) * 8 + (ql >> 3);
+        tj = (gp % gpr) * 32 + (x & 3) * 8 + (ql & 7);
+    } else {
+        ti = blockIdx.x / tiles_j;
+        tj = blockIdx.x % tiles_j;
+        jp = blockIdx.y;
+    }
+}
+
 struct NoIssue {
     __device__ __forceinline__ void operator()(int) const {}
 };
@@ -250,8 +276,8 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     const int tg = wave / (WBI * WBJ);
     const int wb = wave % (WBI * WBJ);
     const int wbi = wb / WBJ, wbj = wb % WBJ;
-    const int ti = blockIdx.x / tiles_j, tj = blockIdx.x % tiles_j;
-    const int jp = blockIdx.y;
+    int ti, tj, jp;
+    tile_of(tiles_j, ti, tj, jp);
     const int i0 = ti * Cfg::BI, j0 = tj * Cfg::BJ;
     const size_t plane = (size_t)np_ * np_;
     const int8_t *Aj = Ah + (size_t)jp * K * PL * plane;
