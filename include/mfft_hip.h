@@ -124,8 +124,9 @@ int  mfh_copy_dev(mfh_ctx *ctx, void *dst, const void *src, size_t bytes);
  * Timing is recorded only while enabled (it adds event records). */
 int  mfh_set_timing(mfh_ctx *ctx, int enable);
 int  mfh_stage_times(const mfh_ctx *ctx, float ms[5]);
-/* Ops/bytes the kernels are designed to: int8 MFMA ops of the pointwise
- * GEMM and the minimum HBM bytes of the transform and carry kernels. */
+/* Ops/bytes the kernels of the most recent product are designed to: int8
+ * MFMA ops of the pointwise GEMM, the minimum HBM bytes of the forward
+ * transforms, and those of the inverse + fold + carry (or decode) stages. */
 int  mfh_work(const mfh_ctx *ctx, double *int8_ops, double *fwd_bytes,
               double *inv_bytes);
 

@@ -99,6 +99,9 @@ struct mfh_ctx {
     void *dInA, *dInB, *dOut;
     size_t inBytes, outBytes;
     size_t bytes;         // device bytes held
+    // last product: output kind (0 limbs, 1 coefficient planes, 2 fp32),
+    // output limbs, whether the carry ran inside the inverse kernel
+    int last_out, last_RL, last_fused;
     // timing
     int timing;
     hipEvent_t ev[5];

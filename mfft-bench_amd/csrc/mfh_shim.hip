@@ -222,6 +222,7 @@ int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut,
     int rc = run_conv(c, kind, dA, dB, c->dCw, 0, 0, (uint16_t *)dOut, RL, &carried);
     if (rc) return rc;
     if (!carried && (rc = mfh_launch_carry(c, c->dCw, (uint16_t *)dOut, RL))) return rc;
+    c->last_out = 0; c->last_RL = RL; c->last_fused = carried;
     mark(c, 4);
     return MFH_OK;
 }
@@ -238,6 +239,7 @@ int mfh_conv_dev(mfh_ctx *c, const void *dA32, const void *dB32, void *dCw)
     select_mode(c, false);
     rc = run_conv(c, MFH_IN_I32, dA32, dB32, (int64_t *)dCw, 0, 0);
     if (rc) return rc;
+    c->last_out = 1; c->last_fused = 0;
     mark(c, 4);
     return MFH_OK;
 }
@@ -249,6 +251,7 @@ int mfh_fpx_mm_dev(mfh_ctx *c, const void *dA, const void *dB, int SA, int SB, v
     int rc = run_conv(c, MFH_IN_F32, dA, dB, c->dCw, SA, SB);
     if (rc) return rc;
     if ((rc = mfh_launch_decode_f32(c, c->dCw, SA + SB, (float *)dC))) return rc;
+    c->last_out = 2; c->last_fused = 0;
     mark(c, 4);
     return MFH_OK;
 }
@@ -382,7 +385,19 @@ int mfh_work(const mfh_ctx *c, double *ops, double *fwd, double *inv)
     const double products = c->mode == MFH_MODE_K7 ? 6.0 : 9.0;
     if (ops) *ops = 2.0 * products * c->NB * (double)c->K * c->K * nnp * c->np;
     if (fwd) *fwd = 2.0 * ((double)c->L * nn * 2.0 + pts * mfh_planes(c->mode) * nnp);
-    if (inv) *inv = pts * nnp * 4.0 * mfh_nclasses(c->mode) + (2.0 * c->L - 1.0) * nn * 8.0;
+    if (inv) {
+        // class results in; then the int64 coefficient planes (written, and
+        // read back by the carry or decode) unless the carry ran inside the
+        // inverse; then the product's output
+        const double cw = (2.0 * c->L - 1.0) * nn * 8.0;
+        double b = pts * nnp * 4.0 * mfh_nclasses(c->mode);
+        if (c->last_out == 1) b += cw;
+        else {
+            if (!c->last_fused) b += 2.0 * cw;
+            b += c->last_out == 2 ? nn * 4.0 : (double)c->last_RL * nn * 2.0;
+        }
+        *inv = b;
+    }
     return MFH_OK;
 }
 
