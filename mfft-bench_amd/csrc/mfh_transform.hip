@@ -486,7 +486,7 @@ __device__ __forceinline__ long long bperm64(long long v, int addr)
 // wave, E <= 64) propagates the carries through the element's 2L-1 planes
 // straight from LDS and writes the RL uint16 output limbs (the semantics of
 // k_carry), saving the int64 round trip through HBM.
-template <int NB, int K, bool CARRY>
+template <int NB, int K, bool CARRY, int NPASS = 2>
 __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict__ C5,
                                                       int64_t *__restrict__ Cw,
                                                       uint16_t *__restrict__ out, int RL,
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
 {
     constexpr int S = K / 2, g = 2 * K / NB, twoK = 2 * K;
     constexpr int PASS = 256 / K;            // elements per pass
-    constexpr int E = 2 * PASS;              // elements per workgroup
+    constexpr int E = NPASS * PASS;          // elements per workgroup
     constexpr int LG = __builtin_ctz(NB);
     extern __shared__ int64_t cwl[];         // [P][E]
     const int tid = threadIdx.x, lane = tid & 63;
@@ -503,7 +503,7 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
     const size_t nn = (size_t)n * n;
     const size_t e0 = (size_t)blockIdx.x * E;
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
+    for (int pass = 0; pass < NPASS; ++pass) {
         const int el = pass * PASS + tid / K;
         const size_t e = e0 + el;
         const bool valid = e < nn;
@@ -865,36 +865,38 @@ int mfh_launch_check_i32(mfh_ctx *c, const int32_t *src, int planes)
 }
 
 namespace {
-template <int NB, int K, bool CARRY>
+template <int NB, int K, bool CARRY, int NPASS = 2>
 bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL)
 {
-    constexpr int E = 2 * (256 / K);
+    constexpr int E = NPASS * (256 / K);
     const int P = 2 * c->L - 1;
     const size_t lds = (size_t)P * E * sizeof(int64_t);
     if (lds > 160 * 1024) return false;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)k_inverse_fast<NB, K, CARRY>,
+        if (hipFuncSetAttribute((const void *)k_inverse_fast<NB, K, CARRY, NPASS>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 160 * 1024) != hipSuccess)
             return false;
         attr_set = true;
     }
     const size_t nn = (size_t)c->n * c->n;
-    hipLaunchKernelGGL((k_inverse_fast<NB, K, CARRY>), dim3((unsigned)((nn + E - 1) / E)),
+    hipLaunchKernelGGL((k_inverse_fast<NB, K, CARRY, NPASS>), dim3((unsigned)((nn + E - 1) / E)),
                        dim3(256), lds, c->stream, c->dC5, Cw, out, RL, c->n, c->np, P, c->mode,
                        mfh_nclasses(c->mode));
     return true;
 }
 // out != nullptr: fused carry into RL uint16 limbs (Cw is not written), for
-// plans with at least 32 elements per workgroup (with fewer, the serial
-// carry lanes cost more than the int64 round trip saves)
+// plans with K <= 16 (with fewer elements per workgroup the serial carry
+// lanes cost more than the int64 round trip saves)
 template <int NB, int K>
 bool try_inverse_fast(mfh_ctx *c, int64_t *Cw, uint16_t *&out, int RL)
 {
     if (c->NB != NB || c->K != K) return false;
+    // with the carry fused, one pass of 256/K elements per workgroup: half
+    // the LDS of two passes, so more workgroups per CU hide the class loads
     if constexpr (2 * (256 / K) >= 32) {
-        if (out) return try_inverse_fast_as<NB, K, true>(c, Cw, out, RL);
+        if (out) return try_inverse_fast_as<NB, K, true, 1>(c, Cw, out, RL);
     }
     out = nullptr;
     return try_inverse_fast_as<NB, K, false>(c, Cw, out, RL);
