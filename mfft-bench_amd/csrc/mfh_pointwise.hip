@@ -48,9 +48,10 @@ constexpr int pmod(int a, int m) { return ((a % m) + m) % m; }
 
 // KB: 64-wide k blocks per LDS fill (1, or 2 for small rings, where one
 // block alone gives too few MFMAs per barrier)
-template <int K_, int T_, int WBI_, int WBJ_, int KB_ = 1>
+// WPE: waves per SIMD the kernel is compiled for (register budget 512/WPE)
+template <int K_, int T_, int WBI_, int WBJ_, int KB_ = 1, int WPE_ = 2>
 struct PwCfg {
-    static constexpr int K = K_, T = T_, WBI = WBI_, WBJ = WBJ_, KB = KB_;
+    static constexpr int K = K_, T = T_, WBI = WBI_, WBJ = WBJ_, KB = KB_, WPE = WPE_;
     static_assert(KB == 1 || KB == 2, "one or two k blocks per fill");
     static constexpr int G = K / T;                 // t-groups per block
     static constexpr int WAVES = WBI * WBJ * G;
@@ -261,7 +262,7 @@ __device__ __forceinline__ void class_pairs(int m, int &rlo, int &npairs)
 // most K * 2^20 each; mfh_create rejects sizes where that reaches 2^31.
 template <class Cfg, int MODE>
 __global__ void __attribute__((amdgpu_flat_work_group_size(Cfg::THREADS, Cfg::THREADS),
-                               amdgpu_waves_per_eu(2, 2)))
+                               amdgpu_waves_per_eu(Cfg::WPE, Cfg::WPE)))
 k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
             int32_t *__restrict__ C5, int np_, int tiles_j)
 {
@@ -410,7 +411,8 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
 template <class Cfg>
 int launch_cfg(mfh_ctx *c)
 {
-    if (c->np % (MFH_KBLK * Cfg::KB)) return MFH_E_UNSUPPORTED;
+    if (c->np % (MFH_KBLK * Cfg::KB) || c->np % Cfg::BI || c->np % Cfg::BJ)
+        return MFH_E_UNSUPPORTED;
     const int tiles_i = c->np / Cfg::BI, tiles_j = c->np / Cfg::BJ;
     static bool attr_set = false;
     if (!attr_set) {
@@ -439,9 +441,11 @@ int mfh_launch_pointwise(mfh_ctx *c)
 {
     switch (c->K) {
     case 4:  return launch_cfg<PwCfg<4, 4, 2, 2>>(c);
+    // K = 8: 8 or 16 waves per workgroup at 4 waves per SIMD (122 / 114
+    // VGPRs); 64 x 32 tiles, or 64 x 64 from n = 4096 on (measured best)
     case 8:
-        return c->np % 128 == 0 ? launch_cfg<PwCfg<8, 8, 2, 2, 2>>(c)
-                                : launch_cfg<PwCfg<8, 8, 2, 2>>(c);
+        return c->np >= 4096 ? launch_cfg<PwCfg<8, 8, 4, 4, 1, 4>>(c)
+                             : launch_cfg<PwCfg<8, 8, 4, 2, 1, 4>>(c);
     case 16: return launch_cfg<PwCfg<16, 16, 2, 2>>(c);
     case 32: return launch_cfg<PwCfg<32, 8, 1, 1>>(c);
     default: return MFH_E_UNSUPPORTED;
