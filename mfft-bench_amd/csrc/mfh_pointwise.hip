@@ -48,10 +48,15 @@ constexpr int pmod(int a, int m) { return ((a % m) + m) % m; }
 
 // KB: 64-wide k blocks per LDS fill (1, or 2 for small rings, where one
 // block alone gives too few MFMAs per barrier)
-// WPE: waves per SIMD the kernel is compiled for (register budget 512/WPE)
-template <int K_, int T_, int WBI_, int WBJ_, int KB_ = 1, int WPE_ = 2>
+// WPE: waves per SIMD the kernel is compiled for (register budget 512/WPE).
+// DMA: fill the round buffer with buffer-to-LDS copies after each round
+// (no staging registers; the fill latency is hidden by the other
+// workgroups on the CU) instead of from registers loaded a round ahead.
+template <int K_, int T_, int WBI_, int WBJ_, int KB_ = 1, int WPE_ = 2, bool DMA_ = false>
 struct PwCfg {
     static constexpr int K = K_, T = T_, WBI = WBI_, WBJ = WBJ_, KB = KB_, WPE = WPE_;
+    static constexpr bool DMA = DMA_;
+    static_assert(!DMA || (KB == 1 && T == K), "copy fills: one k block, whole-ring waves");
     static_assert(KB == 1 || KB == 2, "one or two k blocks per fill");
     static constexpr int G = K / T;                 // t-groups per block
     static constexpr int WAVES = WBI * WBJ * G;
@@ -61,14 +66,21 @@ struct PwCfg {
     static constexpr int B_CHUNKS = K * WBJ * 64;
     static constexpr int SUB_CHUNKS = A_CHUNKS + B_CHUNKS;         // one k block
     static constexpr int LDS_BYTES = KB * SUB_CHUNKS * 16;          // one fill
+    static constexpr int DYN_LDS = DMA ? 0 : LDS_BYTES;   // copy fills use static arrays
 };
 
 // One round: one 64-wide k block of one digit pair, all K values of c2.
 // la points at this wave's A fragment of ring coefficient 0 (stride
 // WBI*64 chunks per coefficient), lb likewise for B.
-template <class Cfg, bool ASC, int T0, class Issue>
+struct NoHook {
+    __device__ __forceinline__ void operator()() const {}
+};
+
+// after_a runs once the wave's A fragments are in registers (T == K only)
+template <class Cfg, bool ASC, int T0, class Issue, class AfterA = NoHook>
 __device__ __forceinline__ void pw_round(v4i (&acc)[Cfg::T], const v4i *__restrict__ la,
-                                         const v4i *__restrict__ lb, const Issue &issue)
+                                         const v4i *__restrict__ lb, const Issue &issue,
+                                         const AfterA &after_a = AfterA{})
 {
     constexpr int K = Cfg::K, T = Cfg::T;
     constexpr int SA = Cfg::WBI * 64, SB = Cfg::WBJ * 64;
@@ -82,6 +94,7 @@ __device__ __forceinline__ void pw_round(v4i (&acc)[Cfg::T], const v4i *__restri
         v4i af[K];
 #pragma unroll
         for (int c1 = 0; c1 < K; ++c1) af[c1] = la[c1 * SA];
+        after_a();
         v4i bq[3];
         bq[0] = lb[(ASC ? 0 : K - 1) * SB];
         if (K > 1) bq[1] = lb[(ASC ? 1 : K - 2) * SB];
@@ -198,6 +211,18 @@ __device__ __forceinline__ void pw_load_round(v4i *buf, const int8_t *a0, const 
                                          0, 0);
 }
 
+// workgroup barrier that waits only for this wave's LDS traffic
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+// workgroup barrier after this wave's global loads (including copies into
+// LDS) and LDS traffic have completed
+__device__ __forceinline__ void round_barrier()
+{
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Workgroup -> (row tile, column tile, point).  Workgroup w runs on XCD
 // w mod 8, and about 512 consecutive workgroups are resident at once (two
 // per CU).  When the tile grid allows, each such group of 512 covers a
@@ -272,6 +297,9 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     constexpr int NA = K * WBI / W, NBF = K * WBJ / W;   // fragments per wave
     static_assert((K * WBI) % W == 0 && (K * WBJ) % W == 0, "fragments split evenly");
     extern __shared__ v4i lds[];
+    // copy fills: A and B tiles in two distinct LDS objects, so that the
+    // compiler can tell a copy into one from reads of the other
+    __shared__ v4i sA[Cfg::DMA ? Cfg::A_CHUNKS : 1], sB[Cfg::DMA ? Cfg::B_CHUNKS : 1];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tg = wave / (WBI * WBJ);
@@ -297,15 +325,41 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     const size_t db = (size_t)(W / WBJ) * PL * plane;
     v4i *wa = lds + wave * 64 + lane;                     // this lane's A slot of fragment f=wave
     v4i *wbp = lds + Cfg::A_CHUNKS + wave * 64 + lane;
-    const v4i *la = lds + wbi * 64 + lane;
-    const v4i *lb = lds + Cfg::A_CHUNKS + wbj * 64 + lane;
+    const v4i *la = (Cfg::DMA ? sA : lds) + wbi * 64 + lane;
+    const v4i *lb = (Cfg::DMA ? sB : lds + Cfg::A_CHUNKS) + wbj * 64 + lane;
     constexpr int KB = Cfg::KB, SUB = Cfg::SUB_CHUNKS, NF = NA + NBF;
     const int kblocks = np_ / (MFH_KBLK * KB);        // fills per digit pair
     const int col = j0 + wbj * 16 + (lane & 15);
     const int row0 = i0 + wbi * 16 + 4 * (lane >> 4);
 
-    v4i R[KB * NF];
+    v4i R[Cfg::DMA ? 1 : KB * NF];
+    // copy fills (DMA mode): the round's A or B tiles straight into LDS
+    auto srcs = [&](RoundPos q, const int8_t *&a0, const int8_t *&b0) {
+        int rlo, np2;
+        class_pairs<MODE>(q.m, rlo, np2);
+        const int r = rlo + q.idx / kblocks, kb = q.idx % kblocks;
+        const int s = MODE == MFH_MODE_K7 ? r : q.m - r;
+        a0 = a_blk + (size_t)r * plane + kb * MFH_KBLK;
+        b0 = b_blk + (size_t)s * plane + kb * MFH_KBLK;
+    };
+    auto dma_a = [&](RoundPos q) {
+        const int8_t *a0, *b0;
+        srcs(q, a0, b0);
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(a0 + i * da),
+                                             (void *)(sA + (wave + i * W) * 64), 16, 0, 0);
+    };
+    auto dma_b = [&](RoundPos q) {
+        const int8_t *a0, *b0;
+        srcs(q, a0, b0);
+#pragma unroll
+        for (int i = 0; i < NBF; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(b0 + i * db),
+                                             (void *)(sB + (wave + i * W) * 64), 16, 0, 0);
+    };
     auto gload = [&](RoundPos q) {
+        if constexpr (Cfg::DMA) return;
         int rlo, np2;
         class_pairs<MODE>(q.m, rlo, np2);
         const int r = rlo + q.idx / kblocks, kb = q.idx % kblocks;
@@ -321,6 +375,7 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
         }
     };
     auto lwrite = [&]() {
+        if constexpr (Cfg::DMA) return;
 #pragma unroll
         for (int sb = 0; sb < KB; ++sb) {
 #pragma unroll
@@ -338,10 +393,15 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
 
     // prologue: round (0,0) into LDS, round after it into registers
     RoundPos cur{0, 0};
-    gload(cur);
-    lwrite();
     RoundPos nxt = next_of(cur);
-    gload(nxt);
+    if constexpr (Cfg::DMA) {
+        dma_a(cur);
+        dma_b(cur);
+    } else {
+        gload(cur);
+        lwrite();
+        gload(nxt);
+    }
     __syncthreads();
 
     v4i acc[T];
@@ -351,6 +411,22 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     // descending pass, which leaves the accumulator's orientation unchanged
     auto step = [&](auto asc_tag) {
         constexpr bool ASC = decltype(asc_tag)::value;
+        if constexpr (Cfg::DMA) {
+            // Once every wave holds its A fragments, the next round's A tile
+            // is copied in while this round's MFMAs run; the B tile follows
+            // after the round.  The last barrier waits for both copies.
+            const bool more = nxt.m < NCLASS;
+            pw_round<Cfg, ASC, 0>(acc, la, lb, NoIssue{}, [&]() {
+                lds_barrier();
+                if (more) dma_a(nxt);
+            });
+            lds_barrier();
+            if (more) dma_b(nxt);
+            round_barrier();
+            cur = nxt;
+            if (cur.m < NCLASS) nxt = next_of(cur);
+            return;
+        }
         if constexpr (KB == 1) {
             pw_dispatch<Cfg, ASC>(tg, acc, la, lb, NoIssue{});
         } else {
@@ -418,19 +494,19 @@ int launch_cfg(mfh_ctx *c)
     if (!attr_set) {
         MFH_HIP(hipFuncSetAttribute((const void *)k_pointwise<Cfg, MFH_MODE_B8>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    Cfg::LDS_BYTES));
+                                    Cfg::DYN_LDS));
         MFH_HIP(hipFuncSetAttribute((const void *)k_pointwise<Cfg, MFH_MODE_K7>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    Cfg::LDS_BYTES));
+                                    Cfg::DYN_LDS));
         attr_set = true;
     }
     dim3 grid((unsigned)(tiles_i * tiles_j), (unsigned)c->NB);
     if (c->mode == MFH_MODE_K7)
         hipLaunchKernelGGL((k_pointwise<Cfg, MFH_MODE_K7>), grid, dim3(Cfg::THREADS),
-                           Cfg::LDS_BYTES, c->stream, c->dAh, c->dBh, c->dC5, c->np, tiles_j);
+                           Cfg::DYN_LDS, c->stream, c->dAh, c->dBh, c->dC5, c->np, tiles_j);
     else
         hipLaunchKernelGGL((k_pointwise<Cfg, MFH_MODE_B8>), grid, dim3(Cfg::THREADS),
-                           Cfg::LDS_BYTES, c->stream, c->dAh, c->dBh, c->dC5, c->np, tiles_j);
+                           Cfg::DYN_LDS, c->stream, c->dAh, c->dBh, c->dC5, c->np, tiles_j);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }
@@ -446,7 +522,8 @@ int mfh_launch_pointwise(mfh_ctx *c)
     case 8:
         return c->np >= 4096 ? launch_cfg<PwCfg<8, 8, 4, 4, 1, 4>>(c)
                              : launch_cfg<PwCfg<8, 8, 4, 2, 1, 4>>(c);
-    case 16: return launch_cfg<PwCfg<16, 16, 2, 2>>(c);
+    // K = 16: copy fills (no staging registers), two workgroups per CU
+    case 16: return launch_cfg<PwCfg<16, 16, 2, 2, 1, 2, true>>(c);
     case 32: return launch_cfg<PwCfg<32, 8, 1, 1>>(c);
     default: return MFH_E_UNSUPPORTED;
     }
