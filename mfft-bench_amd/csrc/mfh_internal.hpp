@@ -23,8 +23,8 @@
 // K*64 terms to an int32 accumulator, i.e. at most K * 2^20 in magnitude.
 // A digit-weight class m = r+s has at most 3 digit pairs, so its int32
 // result is bounded by 3 * (np/64) * K * 2^20, which must stay below 2^31.
-// The pointwise step writes the five class results; the inverse transform
-// recombines C^ = sum_m class_m * 2^(8m) in int64.
+// The pointwise step writes the int32 class results (five for B8, six for
+// K7); the inverse transform recombines them into C^ in int64.
 //
 // int64: |C^| <= K * n * ((NB/2) * 65535)^2, and the inverse transform
 // multiplies by at most NB more; both must stay below 2^62.

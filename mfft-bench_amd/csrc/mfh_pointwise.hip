@@ -11,10 +11,11 @@
 // of T+1 A-planes held in registers, so every operand fragment read from LDS
 // feeds T (or more) MFMAs.
 //
-// Each transformed value is three balanced int8 digits (see
-// mfh_internal.hpp); the products of digit r of A and digit s of B are
-// accumulated in int32 per weight class m = r+s (2^(8m)) and flushed into
-// int64 totals, which are the exact C^_j[t].
+// Each transformed value is split into int8 digit planes (see
+// mfh_internal.hpp: three balanced base-2^8 digits, or three base-2^7 digits
+// and their pairwise sums for Karatsuba); the digit products are
+// accumulated in int32 per weight class and stored per class; the inverse
+// transform recombines the classes into the exact int64 C^_j[t].
 //
 // Signs: the negacyclic wrap (c1 + c2 >= K) subtracts.  An int8 operand
 // cannot be negated (-(-128)), so the wave negates the int32 accumulator
@@ -31,7 +32,9 @@
 // coefficients, a (16*WBI) x 64 tile of A and a (16*WBJ) x 64 tile of B^T
 // into LDS in MFMA operand order (lane l of a 16x64 fragment = row l%16,
 // k bytes 16*(l/16) .. +15; A and B use the same k order, so the dot
-// product is the same whatever order the hardware sums in).
+// product is the same whatever order the hardware sums in).  The next
+// round reaches LDS either through registers loaded a round ahead or by
+// buffer-to-LDS copies issued while this round's MFMAs run (Cfg::DMA).
 //
 // Output: int32 class results in the layout of mfh_c5_index (4 consecutive
 // ring coefficients of 16 consecutive columns are 256 contiguous bytes, so
@@ -277,10 +280,13 @@ __device__ __forceinline__ void class_pairs(int m, int &rlo, int &npairs)
 // point, all K ring coefficients, all five digit-weight classes in turn.
 // Each class's int32 result is stored as soon as the class is complete, so
 // the only long-lived state is one int32 accumulator per (t, element); the
-// kernel fits two workgroups per CU.  Rounds are double-buffered through
-// registers: while a round's MFMAs read the LDS buffer, the next round's
-// fragments stream from global memory into VGPRs; after the round they are
-// written to LDS (one 64 KiB buffer per workgroup).
+// kernel fits two workgroups per CU.  Without Cfg::DMA rounds are
+// double-buffered through registers: while a round's MFMAs read the LDS
+// buffer, the next round's fragments stream from global memory into VGPRs;
+// after the round they are written to LDS (one buffer per workgroup).  With
+// Cfg::DMA the buffer is refilled by buffer-to-LDS copies: the A tile while
+// the round runs (once every wave holds its A fragments), the B tile after
+// it, while the other workgroups on the CU keep the MFMA units busy.
 //
 // Output: class m of (j, i, j', t) at mfh_c5_index + m * mfh_c5_class_stride.
 // Accumulator bound: a class has at most 3 digit pairs x np/64 rounds of at
