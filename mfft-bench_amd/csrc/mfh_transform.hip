@@ -551,13 +551,61 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
     __syncthreads();
     const int ecount = (int)((nn - e0) < (size_t)E ? (nn - e0) : (size_t)E);
     if constexpr (CARRY) {
-        static_assert(E <= 64, "carry lanes must form one wave");
-        if (tid < ecount) {
-            int64_t carry = 0;
-            for (int w = 0; w < RL; ++w) {
-                const int64_t v = carry + (w < P ? cwl[(size_t)w * E + tid] : 0);
-                __builtin_nontemporal_store((uint16_t)(v & 0xFFFF), out + (size_t)w * nn + e0 + tid);
-                carry = v >> 16;
+        // Carry over the RL output limbs by SEGS = 256/E threads per element,
+        // each owning a run of `len` >= 4 consecutive limbs (carry lookahead):
+        //  1. each run propagates its own planes with carry-in 0, giving its
+        //     limbs (value Ls < 2^(16 len)) and carry-out c; with a true
+        //     carry-in X (|X| < 2^47 < 2^(16 len)) the carry-out becomes
+        //     c + floor((Ls + X) / 2^(16 len)), i.e. c + 1 when X >= 2^(16 len)
+        //     - Ls, c - 1 when X < -Ls, else c: two thresholds per run, each
+        //     representable only when Ls is within 2^63 of 0 or 2^(16 len);
+        //  2. one lane per element chains the SEGS runs through them;
+        //  3. each run propagates again from its true carry-in and writes.
+        // Only the last run can be shorter than `len`; its carry-out is the
+        // one discarded (limbs >= RL), so the thresholds never apply to it.
+        constexpr int SEGS = 256 / E;
+        int64_t *segc = cwl + (size_t)P * E;           // [SEGS][E] each
+        int64_t *seglo = segc + SEGS * E, *seghi = seglo + SEGS * E, *segin = seghi + SEGS * E;
+        const int el = tid % E, sg = tid / E;
+        int len = (RL + SEGS - 1) / SEGS;
+        if (len < 4) len = 4;
+        const int w0 = sg * len, w1 = min(w0 + len, RL);
+        {
+            int64_t cc = 0;
+            uint64_t low = 0;                          // limbs 0..3 of the run
+            bool zero_hi = true, ones_hi = true;       // limbs 4.. all 0 / all 0xFFFF
+            for (int w = w0; w < w1; ++w) {
+                const int64_t v = cc + (w < P ? cwl[(size_t)w * E + el] : 0);
+                const uint64_t limb = (uint64_t)(v & 0xFFFF);
+                const int i = w - w0;
+                if (i < 4) low |= limb << (16 * i);
+                else {
+                    zero_hi &= limb == 0;
+                    ones_hi &= limb == 0xFFFF;
+                }
+                cc = v >> 16;
+            }
+            const bool top_clear = (low >> 63) == 0;
+            seglo[sg * E + el] = (zero_hi && top_clear) ? -(int64_t)low : INT64_MIN;
+            seghi[sg * E + el] = (ones_hi && !top_clear && low != (1ull << 63))
+                                     ? (int64_t)(0 - low) : INT64_MAX;
+            segc[sg * E + el] = cc;
+        }
+        __syncthreads();
+        if (tid < E) {
+            int64_t C = 0;
+            for (int r = 0; r < SEGS; ++r) {
+                segin[r * E + tid] = C;
+                C = segc[r * E + tid] + (C >= seghi[r * E + tid]) - (C < seglo[r * E + tid]);
+            }
+        }
+        __syncthreads();
+        if (el < ecount) {
+            int64_t cc = segin[sg * E + el];
+            for (int w = w0; w < w1; ++w) {
+                const int64_t v = cc + (w < P ? cwl[(size_t)w * E + el] : 0);
+                __builtin_nontemporal_store((uint16_t)(v & 0xFFFF), out + (size_t)w * nn + e0 + el);
+                cc = v >> 16;
             }
         }
     } else {
@@ -870,7 +918,8 @@ bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL)
 {
     constexpr int E = NPASS * (256 / K);
     const int P = 2 * c->L - 1;
-    const size_t lds = (size_t)P * E * sizeof(int64_t);
+    // coefficient planes, plus four int64 per carry-run thread
+    const size_t lds = ((size_t)P * E + (CARRY ? 4 * 256 : 0)) * sizeof(int64_t);
     if (lds > 160 * 1024) return false;
     static bool attr_set = false;
     if (!attr_set) {
