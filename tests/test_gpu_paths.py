@@ -110,6 +110,26 @@ def test_all_ones_worst_case(gpu, orc):
             assert np.array_equal(ctx.mm(A, A, RL), want), (n, L)
 
 
+def test_carry_runs_of_ones_and_zeros(gpu):
+    """Products whose limbs are long runs of 0xFFFF or 0x0000: the carry
+    chains cross every carry-lookahead run boundary, in both directions.
+    (-1)(1) summed over n is -n; (-1)(-1) is +n; (2^W - 1)(1) unsigned is
+    n (2^W - 1).  Closed forms, so no oracle is needed."""
+    for n, L in [(64, 128), (16, 64), (32, 32)]:
+        RL = 2 * L + 1
+        ones = np.full(L * n * n, 0xFFFF, np.uint16)             # -1 signed, 2^W-1 unsigned
+        one = np.zeros(L * n * n, np.uint16)
+        one[:n * n] = 1                                            # every entry 1
+        mod = 1 << (16 * RL)
+        cases = [(ones, one, True, (-n) % mod), (ones, ones, True, n),
+                 (ones, one, False, n * ((1 << (16 * L)) - 1))]
+        with gpu.Ctx(n, L) as ctx:
+            for A, B, sgn, val in cases:
+                got = ctx.mm(A, B, RL, signed=sgn).reshape(RL, n * n)
+                want = np.array([(val >> (16 * w)) & 0xFFFF for w in range(RL)], np.uint16)
+                assert np.array_equal(got, np.repeat(want[:, None], n * n, axis=1)), (n, L, sgn)
+
+
 def test_generic_kernels_match(gpu, orc, monkeypatch):
     """The runtime-plan (generic) kernels, forced, give the same bits."""
     monkeypatch.setenv("MFH_GENERIC_KERNELS", "1")
