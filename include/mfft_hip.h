@@ -87,6 +87,13 @@ int mfh_fpx_mm(mfh_ctx *ctx, const float *A, const float *B, int SA, int SB,
                float *C);
 /* decode only: 2L-1 int64 planes -> fp32 with scale 2^-(SA+SB) (device) */
 int mfh_fpx_decode_dev(mfh_ctx *ctx, const void *dCw, int SAB, void *dC);
+/* fp64 on the same grid (src/fpfixed.c:131-173, 308-322): A, B fp64 n x n;
+ * the product is rounded to 53 bits as fpx_decode_f64 does. */
+int mfh_fpx_mm_f64_dev(mfh_ctx *ctx, const void *dA, const void *dB, int SA,
+                       int SB, void *dC);
+int mfh_fpx_mm_f64(mfh_ctx *ctx, const double *A, const double *B, int SA,
+                   int SB, double *C);
+int mfh_fpx_decode_f64_dev(mfh_ctx *ctx, const void *dCw, int SAB, void *dC);
 
 /* ---- standalone host-buffer helpers (temporary device buffers) ---------- */
 /* normalize_planes (src/bigmat.c:48-60) on the device */
@@ -96,6 +103,38 @@ int mfh_normalize(const int64_t *acc, int nplanes, int n, uint16_t *out, int RL)
 int mfh_fpx_encode(const float *X, int n, int L, int S, int32_t *X32);
 /* fpx_decode_f32 (src/fpfixed.c:269-285) of 2L-1 int64 planes */
 int mfh_fpx_decode(const int64_t *Cw, int n, int L, int SAB, float *C);
+/* fpx_encode_d (src/fpfixed.c:144-173): fp64 -> L signed limb planes */
+int mfh_fpx_encode_f64(const double *X, int n, int L, int S, int32_t *X32);
+/* fpx_decode_f64 (src/fpfixed.c:308-322) */
+int mfh_fpx_decode_f64(const int64_t *Cw, int n, int L, int SAB, double *C);
+/* fpx_decode_ld (src/fpfixed.c:292-306): rounding to 63 bits on the device,
+ * C[i] = sig[i] * 2^ex[i] assembled on the host */
+int mfh_fpx_decode_ld(const int64_t *Cw, int n, int L, int SAB, long double *C);
+/* the device half of it: signed 63-bit significands and exponents */
+int mfh_fpx_decode_sig63(const int64_t *Cw, int n, int L, int SAB, int64_t *sig,
+                         int32_t *ex);
+
+/* ---- schoolbook: the leaf operator and the limb-plane method ------------
+ * Integer-ALU kernels, exact modulo 2^64 for any int32 entries (the
+ * reference's int64 leaves wrap the same way); an independent second
+ * computation of every product.  ctx may be NULL (null stream). */
+/* mm_accum (src/kernel.c:1015-1033): C += A*B if sign > 0, else C -= A*B;
+ * int64 C, int32 A, B, all n x n row-major */
+int mfh_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign);
+int mfh_mm_accum_dev(mfh_ctx *ctx, void *dC, const void *dA, const void *dB, int n,
+                     int sign);
+/* conv_limbplane (src/methods.c:94-104): Cw[w] = sum_{u+v=w} A_u B_v over
+ * L limb planes (in_kind MFH_IN_I32: int32, MFH_IN_U16: uint16), 2L-1 int64
+ * planes out */
+int mfh_limbplane_conv(const int32_t *A32, const int32_t *B32, int n, int L, int64_t *Cw);
+int mfh_limbplane_conv_dev(mfh_ctx *ctx, int in_kind, const void *dA, const void *dB,
+                           int n, int L, void *dCw);
+/* mm_limbplane (src/methods.c:106-123): uint16 limb planes, the carry of
+ * the convolution into RL uint16 limbs; dCw is 2L-1 int64 planes of scratch */
+int mfh_limbplane_mm(const uint16_t *A, const uint16_t *B, int n, int L, uint16_t *out,
+                     int RL);
+int mfh_limbplane_mm_dev(mfh_ctx *ctx, const void *dA, const void *dB, int n, int L,
+                         void *dCw, void *dOut, int RL);
 
 /* ---- device memory and timing helpers ----------------------------------- */
 int  mfh_malloc(void **dptr, size_t bytes);

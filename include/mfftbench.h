@@ -59,6 +59,19 @@ void normalize_planes(const int64_t *acc, int nplanes, int n,
 int  bigres_equal(const uint16_t *a, const uint16_t *b, int n, int RL,
                   int *bad_i, int *bad_j, int *bad_w);           /* :62-75 */
 
+/* ---- the leaf operator and the limb-plane schoolbook ---------------------
+ * k must be KERNEL_HIP: integer-ALU kernels on the device, exact modulo 2^64
+ * for any int32 entries like the reference's int64 leaves. */
+/* src/mfftbench.h:53-54: C += A*B if sign > 0, else C -= A*B */
+void mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign,
+              kernel_t k);
+/* src/mfftbench.h:100-101 */
+void mm_limbplane(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
+                  kernel_t k, uint16_t *out, int RL);
+/* src/mfftbench.h:105-106 */
+void conv_limbplane(int64_t *Cw, const int32_t *A32, const int32_t *B32,
+                    int n, int L, kernel_t k);
+
 /* ---- flat MFFT plan (src/mfftbench.h:139-154, src/mfft.c:77-122) -------- */
 typedef struct {
     int L, S, NB, K, g;
@@ -84,7 +97,8 @@ void conv_mfft(int64_t *Cw, const int32_t *A32, const int32_t *B32,
 void mm_mfft_signed(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
                     const mfft_plan *p, kernel_t k, uint16_t *out, int RL);
 
-/* ---- fp32 fixed-point embedding (src/mfftbench.h:182-199, src/fpfixed.c) */
+/* ---- fp32/fp64 fixed-point embedding (src/mfftbench.h:182-199,
+ *      src/fpfixed.c) ------------------------------------------------------ */
 typedef struct {
     int n, L, sig;
     int SA, SB;
@@ -92,17 +106,26 @@ typedef struct {
     int32_t *A32, *B32;     /* signed limb planes, L*n*n each (host)      */
     int64_t *Cw;            /* exact product, 2L-1 int64 planes (host)    */
     double enc_secs, dec_secs;
-    void *dev;              /* device copies of A, B (fpx_mm_f32)         */
+    void *dev;              /* inputs last encoded (fpx_mm_f32/_f64)      */
 } fpx_ctx;
 
-int  fpx_init(fpx_ctx *c, const float *A, const float *B, int n, int force_bits);
-void fpx_encode(fpx_ctx *c, const float *A, const float *B);
-void fpx_decode_f32(fpx_ctx *c, float *C);
-void fpx_free(fpx_ctx *c);
+int  fpx_init(fpx_ctx *c, const float *A, const float *B, int n,
+              int force_bits);                                          /* :191 */
+void fpx_encode(fpx_ctx *c, const float *A, const float *B);            /* :192 */
+int  fpx_init_d(fpx_ctx *c, const double *A, const double *B, int n,
+                int force_bits);                                        /* :193 */
+void fpx_encode_d(fpx_ctx *c, const double *A, const double *B);        /* :195 */
+void fpx_decode_ld(fpx_ctx *c, long double *C);                         /* :196 */
+void fpx_decode_f32(fpx_ctx *c, float *C);                              /* :197 */
+void fpx_decode_f64(fpx_ctx *c, double *C);                             /* :198 */
+void fpx_free(fpx_ctx *c);                                              /* :199 */
 /* encode -> MFFT product -> decode entirely on the device, from the fp32
  * matrices given to fpx_encode (no reference counterpart; equals
  * conv_mfft + fpx_decode_f32 bit for bit). */
 int  fpx_mm_f32(fpx_ctx *c, const mfft_plan *p, float *C);
+/* the same for fp64 matrices given to fpx_encode_d (equals conv_mfft +
+ * fpx_decode_f64 bit for bit; no reference counterpart) */
+int  fpx_mm_f64(fpx_ctx *c, const mfft_plan *p, double *C);
 
 /* Status of the most recent call on this thread: 0, or a negative code
  * from mfft_hip.h (MFH_E_*). */

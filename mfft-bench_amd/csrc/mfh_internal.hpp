@@ -121,16 +121,30 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carr
 int mfh_launch_carry(mfh_ctx *c, const int64_t *Cw, uint16_t *out, int RL);
 int mfh_launch_carry_planes(const int64_t *Cw, int P, size_t nn, uint16_t *out,
                             int RL, hipStream_t st);
-int mfh_launch_encode_f32(const float *X, int n, int L, int S, int32_t *out,
-                          hipStream_t st);
-int mfh_launch_decode_f32(mfh_ctx *c, const int64_t *Cw, int SAB, float *out);
+// fp32 (is_f64 = 0) or fp64 matrix -> L signed limb planes at scale 2^S
+int mfh_launch_encode(const void *X, int is_f64, int n, int L, int S, int32_t *out,
+                      hipStream_t st);
+// 2L-1 coefficient planes -> floats at scale 2^-SAB (fmt: MFH_DEC_*)
+int mfh_launch_decode(mfh_ctx *c, const int64_t *Cw, int SAB, int fmt, void *out,
+                      int32_t *out2);
 int mfh_launch_rand_u16(void *dst, size_t count, uint64_t seed, hipStream_t st);
+// schoolbook (mfh_limbplane.hip): C += sign A B; Cw[w] = sum_{u+v=w} A_u B_v
+// over uint16 (u16 != 0) or int32 limb planes
+int mfh_launch_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign,
+                        hipStream_t st);
+int mfh_launch_conv_limbplane(int64_t *Cw, const void *A, const void *B, int u16, int n, int L,
+                              hipStream_t st);
 int mfh_launch_copy16(void *dst, const void *src, size_t bytes, hipStream_t st);
 int mfh_launch_rand_f32(void *dst, size_t count, uint64_t seed, int emin,
                         int emax, hipStream_t st);
 
-// input kind used internally for fp32 sources
+// input kinds used internally for fixed-point float sources
 #define MFH_IN_F32 100
+#define MFH_IN_F64 101
+// decode formats: fp32, fp64, 63-bit significand + exponent (long double)
+#define MFH_DEC_F32 0
+#define MFH_DEC_F64 1
+#define MFH_DEC_SIG63 2
 
 #define MFH_HIP(call)                                   \
     do {                                                \

@@ -1,0 +1,153 @@
+// mfh_limbplane.hip -- the schoolbook side of the library on gfx950: the leaf
+// operator mm_accum (C += sign * A * B on int32 n x n matrices, int64 C) and
+// the limb-plane convolution
+//     Cw[w] = sum_{u+v=w} A_u B_v,   w = 0 .. 2L-2      (src/methods.c:94-104)
+// as one batched launch.  Both are exact modulo 2^64, like the reference's
+// int64 leaves (src/kernel.c:132-158): every product of two int32 values is
+// formed exactly in 64 bits and the sums wrap, so the result does not
+// depend on the order of summation.
+//
+// These run on the integer vector ALU (v_mad_i64_i32 class instructions),
+// not on the int8 matrix cores: any int32 entry is accepted, which the
+// digit-split MFMA path cannot do, so the schoolbook stays an independent
+// second computation of every product the MFFT path makes.
+//
+// Tiling: a 256-thread workgroup owns a 64 x 64 output tile; each thread
+// owns a 4 x 4 block (rows 4*(tid/16).., columns 4*(tid%16)..).  The k
+// dimension is walked in slices of 32: the A slice is stored transposed in
+// LDS (As[k][row]) and the B slice as is (Bs[k][col]), so a thread reads
+// four consecutive rows and four consecutive columns with two 16-byte LDS
+// loads per k and issues 16 multiply-adds.  Rows padded by 4 ints keep the
+// transposed stores of A off a single bank.
+#include "mfh_internal.hpp"
+
+namespace {
+
+constexpr int TI = 64, TK = 32, PADW = TI + 4;
+
+template <class T>
+__device__ __forceinline__ int load_in(const T *p, size_t off) { return (int)p[off]; }
+
+// one k slice of A (rows i0.., cols k0..) and of B (rows k0.., cols j0..)
+// into LDS; zero outside the n x n matrices
+template <class T>
+__device__ __forceinline__ void stage(int (*As)[PADW], int (*Bs)[PADW], const T *__restrict__ A,
+                                      const T *__restrict__ B, int n, int i0, int j0, int k0)
+{
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < (TI * TK) / 256; ++r) {
+        const int idx = tid + 256 * r;
+        // A: 32 consecutive k of one row per 32 threads (coalesced reads)
+        const int ar = idx / TK, ak = idx % TK;
+        const int gi = i0 + ar, gk = k0 + ak;
+        As[ak][ar] = (gi < n && gk < n) ? load_in(A, (size_t)gi * n + gk) : 0;
+        // B: 64 consecutive columns of one k row per 64 threads
+        const int bk = idx / TI, bc = idx % TI;
+        const int gkb = k0 + bk, gj = j0 + bc;
+        Bs[bk][bc] = (gkb < n && gj < n) ? load_in(B, (size_t)gkb * n + gj) : 0;
+    }
+}
+
+__device__ __forceinline__ void mac_slice(unsigned long long (&acc)[4][4], int (*As)[PADW],
+                                          int (*Bs)[PADW], int r0, int c0)
+{
+#pragma unroll 8
+    for (int kk = 0; kk < TK; ++kk) {
+        const int4 a = *(const int4 *)&As[kk][r0];
+        const int4 b = *(const int4 *)&Bs[kk][c0];
+        const int av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+            for (int y = 0; y < 4; ++y)
+                acc[x][y] += (unsigned long long)((long long)av[x] * (long long)bv[y]);
+    }
+}
+
+// C += sign * A * B (sign > 0 adds, otherwise subtracts: src/kernel.c:157)
+__global__ __launch_bounds__(256) void k_mm_accum(long long *__restrict__ C,
+                                                  const int32_t *__restrict__ A,
+                                                  const int32_t *__restrict__ B, int n, int sign)
+{
+    __shared__ __align__(16) int As[TK][PADW];
+    __shared__ __align__(16) int Bs[TK][PADW];
+    const int i0 = blockIdx.y * TI, j0 = blockIdx.x * TI;
+    const int r0 = 4 * (threadIdx.x / 16), c0 = 4 * (threadIdx.x % 16);
+    unsigned long long acc[4][4] = {};
+    for (int k0 = 0; k0 < n; k0 += TK) {
+        stage(As, Bs, A, B, n, i0, j0, k0);
+        __syncthreads();
+        mac_slice(acc, As, Bs, r0, c0);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) {
+            const int i = i0 + r0 + x, j = j0 + c0 + y;
+            if (i < n && j < n) {
+                unsigned long long *p = (unsigned long long *)&C[(size_t)i * n + j];
+                *p = sign > 0 ? *p + acc[x][y] : *p - acc[x][y];
+            }
+        }
+}
+
+// Cw[w] for w = blockIdx.z: sum over the limb pairs (u, w-u) inside [0, L)
+template <class T>
+__global__ __launch_bounds__(256) void k_conv_limbplane(long long *__restrict__ Cw,
+                                                        const T *__restrict__ A,
+                                                        const T *__restrict__ B, int n, int L)
+{
+    __shared__ __align__(16) int As[TK][PADW];
+    __shared__ __align__(16) int Bs[TK][PADW];
+    const size_t nn = (size_t)n * n;
+    const int w = blockIdx.z;
+    const int i0 = blockIdx.y * TI, j0 = blockIdx.x * TI;
+    const int r0 = 4 * (threadIdx.x / 16), c0 = 4 * (threadIdx.x % 16);
+    const int ulo = w - L + 1 > 0 ? w - L + 1 : 0, uhi = w < L - 1 ? w : L - 1;
+    unsigned long long acc[4][4] = {};
+    for (int u = ulo; u <= uhi; ++u) {
+        const T *Au = A + (size_t)u * nn, *Bv = B + (size_t)(w - u) * nn;
+        for (int k0 = 0; k0 < n; k0 += TK) {
+            stage(As, Bs, Au, Bv, n, i0, j0, k0);
+            __syncthreads();
+            mac_slice(acc, As, Bs, r0, c0);
+            __syncthreads();
+        }
+    }
+    long long *Cout = Cw + (size_t)w * nn;
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int y = 0; y < 4; ++y) {
+            const int i = i0 + r0 + x, j = j0 + c0 + y;
+            if (i < n && j < n) Cout[(size_t)i * n + j] = (long long)acc[x][y];
+        }
+}
+
+}  // namespace
+
+int mfh_launch_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign,
+                        hipStream_t st)
+{
+    const unsigned t = (unsigned)((n + TI - 1) / TI);
+    hipLaunchKernelGGL(k_mm_accum, dim3(t, t), dim3(256), 0, st, (long long *)C, A, B, n, sign);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_conv_limbplane(int64_t *Cw, const void *A, const void *B, int u16, int n, int L,
+                              hipStream_t st)
+{
+    const unsigned t = (unsigned)((n + TI - 1) / TI);
+    const dim3 grid(t, t, (unsigned)(2 * L - 1));
+    if (u16)
+        hipLaunchKernelGGL(k_conv_limbplane<uint16_t>, grid, dim3(256), 0, st, (long long *)Cw,
+                           (const uint16_t *)A, (const uint16_t *)B, n, L);
+    else
+        hipLaunchKernelGGL(k_conv_limbplane<int32_t>, grid, dim3(256), 0, st, (long long *)Cw,
+                           (const int32_t *)A, (const int32_t *)B, n, L);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}

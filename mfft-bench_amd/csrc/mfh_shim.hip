@@ -94,8 +94,9 @@ int run_conv(mfh_ctx *c, int kind, const void *dA, const void *dB, int64_t *Cw,
 {
     int rc;
     mark(c, 0);
-    const int eb = (kind == MFH_IN_U16 || kind == MFH_IN_U16_SIGNED) ? 2 : 4;
-    const int planes = kind == MFH_IN_F32 ? 1 : c->L;
+    const int eb = (kind == MFH_IN_U16 || kind == MFH_IN_U16_SIGNED) ? 2
+                   : kind == MFH_IN_F64 ? 8 : 4;
+    const int planes = (kind == MFH_IN_F32 || kind == MFH_IN_F64) ? 1 : c->L;
     if ((rc = mfh_launch_transpose(dB, c->dBt, planes, c->n, eb, c->stream))) return rc;
     if ((rc = mfh_launch_forward(c, kind, dA, c->dAh, SA))) return rc;
     if ((rc = mfh_launch_forward(c, kind, c->dBt, c->dBh, SB))) return rc;
@@ -244,22 +245,43 @@ int mfh_conv_dev(mfh_ctx *c, const void *dA32, const void *dB32, void *dCw)
     return MFH_OK;
 }
 
-int mfh_fpx_mm_dev(mfh_ctx *c, const void *dA, const void *dB, int SA, int SB, void *dC)
+namespace {
+// encode -> product -> decode of fp32 (f64 = 0) or fp64 matrices
+int fpx_mm_dev(mfh_ctx *c, int f64, const void *dA, const void *dB, int SA, int SB, void *dC)
 {
     if (!c || !dA || !dB || !dC) return MFH_E_ARG;
     select_mode(c, false);
-    int rc = run_conv(c, MFH_IN_F32, dA, dB, c->dCw, SA, SB);
+    int rc = run_conv(c, f64 ? MFH_IN_F64 : MFH_IN_F32, dA, dB, c->dCw, SA, SB);
     if (rc) return rc;
-    if ((rc = mfh_launch_decode_f32(c, c->dCw, SA + SB, (float *)dC))) return rc;
-    c->last_out = 2; c->last_fused = 0;
+    if ((rc = mfh_launch_decode(c, c->dCw, SA + SB, f64 ? MFH_DEC_F64 : MFH_DEC_F32, dC,
+                                nullptr)))
+        return rc;
+    c->last_out = f64 ? 3 : 2; c->last_fused = 0;
     mark(c, 4);
     return MFH_OK;
+}
+}  // namespace
+
+int mfh_fpx_mm_dev(mfh_ctx *c, const void *dA, const void *dB, int SA, int SB, void *dC)
+{
+    return fpx_mm_dev(c, 0, dA, dB, SA, SB, dC);
+}
+
+int mfh_fpx_mm_f64_dev(mfh_ctx *c, const void *dA, const void *dB, int SA, int SB, void *dC)
+{
+    return fpx_mm_dev(c, 1, dA, dB, SA, SB, dC);
 }
 
 int mfh_fpx_decode_dev(mfh_ctx *c, const void *dCw, int SAB, void *dC)
 {
     if (!c || !dCw || !dC) return MFH_E_ARG;
-    return mfh_launch_decode_f32(c, (const int64_t *)dCw, SAB, (float *)dC);
+    return mfh_launch_decode(c, (const int64_t *)dCw, SAB, MFH_DEC_F32, dC, nullptr);
+}
+
+int mfh_fpx_decode_f64_dev(mfh_ctx *c, const void *dCw, int SAB, void *dC)
+{
+    if (!c || !dCw || !dC) return MFH_E_ARG;
+    return mfh_launch_decode(c, (const int64_t *)dCw, SAB, MFH_DEC_F64, dC, nullptr);
 }
 
 int mfh_mm(mfh_ctx *c, int kind, const uint16_t *A, const uint16_t *B, uint16_t *out, int RL)
@@ -293,18 +315,30 @@ int mfh_conv(mfh_ctx *c, const int32_t *A32, const int32_t *B32, int64_t *Cw)
     return MFH_OK;
 }
 
-int mfh_fpx_mm(mfh_ctx *c, const float *A, const float *B, int SA, int SB, float *C)
+namespace {
+int fpx_mm_host(mfh_ctx *c, int f64, const void *A, const void *B, int SA, int SB, void *C)
 {
     if (!c || !A || !B || !C) return MFH_E_ARG;
-    const size_t nn = (size_t)c->n * c->n;
-    int rc = ensure_staging(c, nn * 4, nn * 4);
+    const size_t nn = (size_t)c->n * c->n, eb = f64 ? 8 : 4;
+    int rc = ensure_staging(c, nn * eb, nn * eb);
     if (rc) return rc;
-    MFH_HIP(hipMemcpyAsync(c->dInA, A, nn * 4, hipMemcpyHostToDevice, c->stream));
-    MFH_HIP(hipMemcpyAsync(c->dInB, B, nn * 4, hipMemcpyHostToDevice, c->stream));
-    if ((rc = mfh_fpx_mm_dev(c, c->dInA, c->dInB, SA, SB, c->dOut))) return rc;
-    MFH_HIP(hipMemcpyAsync(C, c->dOut, nn * 4, hipMemcpyDeviceToHost, c->stream));
+    MFH_HIP(hipMemcpyAsync(c->dInA, A, nn * eb, hipMemcpyHostToDevice, c->stream));
+    MFH_HIP(hipMemcpyAsync(c->dInB, B, nn * eb, hipMemcpyHostToDevice, c->stream));
+    if ((rc = fpx_mm_dev(c, f64, c->dInA, c->dInB, SA, SB, c->dOut))) return rc;
+    MFH_HIP(hipMemcpyAsync(C, c->dOut, nn * eb, hipMemcpyDeviceToHost, c->stream));
     MFH_HIP(hipStreamSynchronize(c->stream));
     return MFH_OK;
+}
+}  // namespace
+
+int mfh_fpx_mm(mfh_ctx *c, const float *A, const float *B, int SA, int SB, float *C)
+{
+    return fpx_mm_host(c, 0, A, B, SA, SB, C);
+}
+
+int mfh_fpx_mm_f64(mfh_ctx *c, const double *A, const double *B, int SA, int SB, double *C)
+{
+    return fpx_mm_host(c, 1, A, B, SA, SB, C);
 }
 
 int mfh_malloc(void **p, size_t bytes)
@@ -394,7 +428,8 @@ int mfh_work(const mfh_ctx *c, double *ops, double *fwd, double *inv)
         if (c->last_out == 1) b += cw;
         else {
             if (!c->last_fused) b += 2.0 * cw;
-            b += c->last_out == 2 ? nn * 4.0 : (double)c->last_RL * nn * 2.0;
+            b += c->last_out == 2 ? nn * 4.0 : c->last_out == 3 ? nn * 8.0
+                                                 : (double)c->last_RL * nn * 2.0;
         }
         *inv = b;
     }
@@ -437,41 +472,179 @@ int mfh_normalize(const int64_t *acc, int nplanes, int n, uint16_t *out, int RL)
     return MFH_OK;
 }
 
-int mfh_fpx_encode(const float *X, int n, int L, int S, int32_t *X32)
+namespace {
+int encode_host(const void *X, int f64, int n, int L, int S, int32_t *X32)
 {
     if (!X || !X32 || n < 1 || L < 1) return MFH_E_ARG;
     int rc = check_device();
     if (rc) return rc;
-    const size_t nn = (size_t)n * n;
+    const size_t nn = (size_t)n * n, eb = f64 ? 8 : 4;
     TmpBufs t;
-    if (hipMalloc(&t.p[0], nn * 4) != hipSuccess ||
+    if (hipMalloc(&t.p[0], nn * eb) != hipSuccess ||
         hipMalloc(&t.p[1], (size_t)L * nn * 4) != hipSuccess)
         return MFH_E_NOMEM;
-    MFH_HIP(hipMemcpy(t.p[0], X, nn * 4, hipMemcpyHostToDevice));
-    if ((rc = mfh_launch_encode_f32((const float *)t.p[0], n, L, S, (int32_t *)t.p[1], 0)))
-        return rc;
+    MFH_HIP(hipMemcpy(t.p[0], X, nn * eb, hipMemcpyHostToDevice));
+    if ((rc = mfh_launch_encode(t.p[0], f64, n, L, S, (int32_t *)t.p[1], 0))) return rc;
     MFH_HIP(hipMemcpy(X32, t.p[1], (size_t)L * nn * 4, hipMemcpyDeviceToHost));
     return MFH_OK;
 }
 
-int mfh_fpx_decode(const int64_t *Cw, int n, int L, int SAB, float *C)
+// decode of host coefficient planes; out gets nn values of `out_bytes` each
+// (SIG63: int64 significands, exponents to out2)
+int decode_host(const int64_t *Cw, int n, int L, int SAB, int fmt, void *out,
+                size_t out_bytes, int32_t *out2)
 {
-    if (!Cw || !C || n < 1 || L < 1) return MFH_E_ARG;
+    if (!Cw || !out || n < 1 || L < 1) return MFH_E_ARG;
     int rc = check_device();
     if (rc) return rc;
     const size_t nn = (size_t)n * n;
     TmpBufs t;
     if (hipMalloc(&t.p[0], (size_t)(2 * L - 1) * nn * 8) != hipSuccess ||
-        hipMalloc(&t.p[1], nn * 4) != hipSuccess)
+        hipMalloc(&t.p[1], nn * out_bytes) != hipSuccess ||
+        (out2 && hipMalloc(&t.p[2], nn * 4) != hipSuccess))
         return MFH_E_NOMEM;
     MFH_HIP(hipMemcpy(t.p[0], Cw, (size_t)(2 * L - 1) * nn * 8, hipMemcpyHostToDevice));
     mfh_ctx c;
     bare_ctx(c, n, L);
-    if ((rc = mfh_launch_decode_f32(&c, (const int64_t *)t.p[0], SAB, (float *)t.p[1])))
+    if ((rc = mfh_launch_decode(&c, (const int64_t *)t.p[0], SAB, fmt, t.p[1],
+                                (int32_t *)t.p[2])))
         return rc;
     MFH_HIP(hipDeviceSynchronize());
-    MFH_HIP(hipMemcpy(C, t.p[1], nn * 4, hipMemcpyDeviceToHost));
+    MFH_HIP(hipMemcpy(out, t.p[1], nn * out_bytes, hipMemcpyDeviceToHost));
+    if (out2) MFH_HIP(hipMemcpy(out2, t.p[2], nn * 4, hipMemcpyDeviceToHost));
     return MFH_OK;
+}
+}  // namespace
+
+int mfh_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign)
+{
+    if (!C || !A || !B || n < 1) return MFH_E_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t nn = (size_t)n * n;
+    TmpBufs t;
+    if (hipMalloc(&t.p[0], nn * 8) != hipSuccess || hipMalloc(&t.p[1], nn * 4) != hipSuccess ||
+        hipMalloc(&t.p[2], nn * 4) != hipSuccess)
+        return MFH_E_NOMEM;
+    MFH_HIP(hipMemcpy(t.p[0], C, nn * 8, hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(t.p[1], A, nn * 4, hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(t.p[2], B, nn * 4, hipMemcpyHostToDevice));
+    if ((rc = mfh_launch_mm_accum((int64_t *)t.p[0], (const int32_t *)t.p[1],
+                                  (const int32_t *)t.p[2], n, sign, 0)))
+        return rc;
+    MFH_HIP(hipDeviceSynchronize());
+    MFH_HIP(hipMemcpy(C, t.p[0], nn * 8, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+
+int mfh_mm_accum_dev(mfh_ctx *c, void *dC, const void *dA, const void *dB, int n, int sign)
+{
+    if (!dC || !dA || !dB || n < 1) return MFH_E_ARG;
+    return mfh_launch_mm_accum((int64_t *)dC, (const int32_t *)dA, (const int32_t *)dB, n, sign,
+                               c ? c->stream : 0);
+}
+
+int mfh_limbplane_conv_dev(mfh_ctx *c, int in_kind, const void *dA, const void *dB, int n,
+                           int L, void *dCw)
+{
+    if (!dA || !dB || !dCw || n < 1 || L < 1) return MFH_E_ARG;
+    if (in_kind != MFH_IN_U16 && in_kind != MFH_IN_I32) return MFH_E_ARG;
+    return mfh_launch_conv_limbplane((int64_t *)dCw, dA, dB, in_kind == MFH_IN_U16, n, L,
+                                     c ? c->stream : 0);
+}
+
+int mfh_limbplane_mm_dev(mfh_ctx *c, const void *dA, const void *dB, int n, int L, void *dCw,
+                         void *dOut, int RL)
+{
+    if (!dOut || RL < 1) return MFH_E_ARG;
+    int rc = mfh_limbplane_conv_dev(c, MFH_IN_U16, dA, dB, n, L, dCw);
+    if (rc) return rc;
+    return mfh_launch_carry_planes((const int64_t *)dCw, 2 * L - 1, (size_t)n * n,
+                                   (uint16_t *)dOut, RL, c ? c->stream : 0);
+}
+
+namespace {
+// conv_limbplane / mm_limbplane on host buffers: limb planes in, the 2L-1
+// coefficient planes (out == nullptr) or RL carried limbs out
+int limbplane_host(int in_kind, const void *A, const void *B, int n, int L, int64_t *Cw,
+                   uint16_t *out, int RL)
+{
+    if (!A || !B || n < 1 || L < 1 || (!Cw && (!out || RL < 1))) return MFH_E_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t nn = (size_t)n * n, eb = in_kind == MFH_IN_U16 ? 2 : 4;
+    const size_t cw_b = (size_t)(2 * L - 1) * nn * 8;
+    TmpBufs t;
+    void *dOut = nullptr;
+    if (hipMalloc(&t.p[0], (size_t)L * nn * eb) != hipSuccess ||
+        hipMalloc(&t.p[1], (size_t)L * nn * eb) != hipSuccess ||
+        hipMalloc(&t.p[2], cw_b + (out ? (size_t)RL * nn * 2 : 0)) != hipSuccess)
+        return MFH_E_NOMEM;
+    if (out) dOut = (char *)t.p[2] + cw_b;
+    MFH_HIP(hipMemcpy(t.p[0], A, (size_t)L * nn * eb, hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(t.p[1], B, (size_t)L * nn * eb, hipMemcpyHostToDevice));
+    rc = out ? mfh_limbplane_mm_dev(nullptr, t.p[0], t.p[1], n, L, t.p[2], dOut, RL)
+             : mfh_limbplane_conv_dev(nullptr, in_kind, t.p[0], t.p[1], n, L, t.p[2]);
+    if (rc) return rc;
+    MFH_HIP(hipDeviceSynchronize());
+    if (out) MFH_HIP(hipMemcpy(out, dOut, (size_t)RL * nn * 2, hipMemcpyDeviceToHost));
+    else MFH_HIP(hipMemcpy(Cw, t.p[2], cw_b, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+}  // namespace
+
+int mfh_limbplane_conv(const int32_t *A32, const int32_t *B32, int n, int L, int64_t *Cw)
+{
+    if (!Cw) return MFH_E_ARG;
+    return limbplane_host(MFH_IN_I32, A32, B32, n, L, Cw, nullptr, 0);
+}
+
+int mfh_limbplane_mm(const uint16_t *A, const uint16_t *B, int n, int L, uint16_t *out, int RL)
+{
+    if (!out) return MFH_E_ARG;
+    return limbplane_host(MFH_IN_U16, A, B, n, L, nullptr, out, RL);
+}
+
+int mfh_fpx_encode(const float *X, int n, int L, int S, int32_t *X32)
+{
+    return encode_host(X, 0, n, L, S, X32);
+}
+
+int mfh_fpx_encode_f64(const double *X, int n, int L, int S, int32_t *X32)
+{
+    return encode_host(X, 1, n, L, S, X32);
+}
+
+int mfh_fpx_decode(const int64_t *Cw, int n, int L, int SAB, float *C)
+{
+    return decode_host(Cw, n, L, SAB, MFH_DEC_F32, C, 4, nullptr);
+}
+
+int mfh_fpx_decode_f64(const int64_t *Cw, int n, int L, int SAB, double *C)
+{
+    return decode_host(Cw, n, L, SAB, MFH_DEC_F64, C, 8, nullptr);
+}
+
+int mfh_fpx_decode_sig63(const int64_t *Cw, int n, int L, int SAB, int64_t *sig, int32_t *ex)
+{
+    if (!ex) return MFH_E_ARG;
+    return decode_host(Cw, n, L, SAB, MFH_DEC_SIG63, sig, 8, ex);
+}
+
+int mfh_fpx_decode_ld(const int64_t *Cw, int n, int L, int SAB, long double *C)
+{
+    if (!C || n < 1) return MFH_E_ARG;
+    const size_t nn = (size_t)n * n;
+    int64_t *sig = (int64_t *)malloc(nn * 8);
+    int32_t *ex = (int32_t *)malloc(nn * 4);
+    int rc = (sig && ex) ? mfh_fpx_decode_sig63(Cw, n, L, SAB, sig, ex) : MFH_E_NOMEM;
+    // the significand has at most 63 bits and the scale stays far inside
+    // the long double exponent range, so this conversion is exact
+    if (!rc)
+        for (size_t i = 0; i < nn; ++i) C[i] = sig[i] ? ldexpl((long double)sig[i], ex[i]) : 0.0L;
+    free(sig);
+    free(ex);
+    return rc;
 }
 
 }  // extern "C"

@@ -1,6 +1,7 @@
 // mfh_transform.hip -- bandwidth-side kernels of the gfx950 MFFT matmul:
 // forward ring transform with digit split, inverse transform + fold, carry
-// normalisation, fp32 decode, plane transpose and seeded input generators.
+// normalisation, fixed-point float encode/decode, plane transpose and seeded
+// input generators.
 //
 // Ring R = Z[y]/(y^K + 1); omega = y^g is a primitive NB-th root of unity
 // (g = 2K/NB).  A matrix element's L limbs form NB/2 non-zero blocks of S
@@ -54,6 +55,7 @@ struct SrcI32 {
 // exact 24-bit integer, and the value mi << (e - 24 + S) lands in limbs
 // lo .. lo+2 with lo = (e-24+S) >> 4.
 struct SrcF32 {
+    static constexpr int NW = 3;   // limbs one entry can touch
     const float *p;
     size_t nn;
     int n, L, S;
@@ -71,6 +73,62 @@ struct SrcF32 {
         unsigned long long v = (unsigned long long)mi << (off & 15);
         int limb = (int)((v >> (16 * t)) & 0xFFFFu);
         return x < 0.0f ? -limb : limb;
+    }
+    // the entry's limbs lo .. lo+2 (lo = L when it has none on the grid)
+    __device__ void window(int i, int k, int &lo, int r[NW]) const
+    {
+        lo = L;
+        for (int t = 0; t < NW; ++t) r[t] = 0;
+        float x = p[(size_t)i * n + k];
+        if (x == 0.0f || !isfinite(x)) return;
+        int e;
+        float m = frexpf(x, &e);
+        int mi = (int)(fabsf(m) * 16777216.0f);
+        int off = e - 24 + S;
+        if (off < 0) return;
+        lo = off >> 4;
+        unsigned long long v = (unsigned long long)mi << (off & 15);
+        for (int t = 0; t < NW; ++t) {
+            int limb = (int)((v >> (16 * t)) & 0xFFFFu);
+            r[t] = x < 0.0f ? -limb : limb;
+        }
+    }
+};
+
+// fp64 on the grid (src/fpfixed.c:144-162): mi = |m| 2^53 is an exact
+// 53-bit integer; shifted by up to 15 it spans 68 bits, i.e. limbs
+// lo .. lo+4.  The shift is done on a 128-bit pair (hi:lo words).
+struct SrcF64 {
+    static constexpr int NW = 5;
+    const double *p;
+    size_t nn;
+    int n, L, S;
+    __device__ void window(int i, int k, int &lo, int r[NW]) const
+    {
+        lo = L;
+        for (int t = 0; t < NW; ++t) r[t] = 0;
+        double x = p[(size_t)i * n + k];
+        if (x == 0.0 || !isfinite(x)) return;
+        int e;
+        double m = frexp(x, &e);
+        unsigned long long mi = (unsigned long long)(fabs(m) * 9007199254740992.0);
+        int off = e - 53 + S;
+        if (off < 0) return;
+        lo = off >> 4;
+        const int sh = off & 15;
+        const unsigned long long w0 = mi << sh, w1 = sh ? mi >> (64 - sh) : 0ull;
+        for (int t = 0; t < NW; ++t) {
+            int limb = (int)((t < 4 ? w0 >> (16 * t) : w1) & 0xFFFFu);
+            r[t] = x < 0.0 ? -limb : limb;
+        }
+    }
+    __device__ int get(int u, int i, int k) const
+    {
+        int lo, r[NW];
+        window(i, k, lo, r);
+        int v = 0;
+        for (int t = 0; t < NW; ++t) v = u == lo + t ? r[t] : v;
+        return v;
     }
 };
 
@@ -151,6 +209,46 @@ __global__ __launch_bounds__(256) void k_forward_generic(
                     else if (s >= K && s < K + S) acc -= src.get(b * S + s - K, i, k);
                 }
             }
+            constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
+            store_digits<MODE>(out + ((size_t)(j * K + c) * PL) * nnp + e, nnp, acc);
+        }
+    }
+}
+
+// ---- forward transform of fixed-point floats, generic plan ---------------------
+// An fp32/fp64 entry has at most NW non-zero limbs (a window lo .. lo+NW-1),
+// so each output coefficient is a signed selection among NW values: limb
+// u = b S + s lands, at point j, on ring position p = s + g j b (mod 2K),
+// with a sign flip when p >= K.  Limbs at or above L are dropped, as the
+// encoder drops them (src/fpfixed.c:155-156).
+template <class Src, int MODE>
+__global__ __launch_bounds__(256) void k_forward_window(Src src, int8_t *__restrict__ out,
+                                                        int np_, int S, int NB, int K, int g)
+{
+    constexpr int NW = Src::NW;
+    const size_t nnp = (size_t)np_ * np_;
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= nnp) return;
+    const int i = (int)(e / np_), k = (int)(e % np_);
+    int lo = src.L, r[NW];
+    if (i < src.n && k < src.n) src.window(i, k, lo, r);
+    int b[NW], s[NW];
+#pragma unroll
+    for (int t = 0; t < NW; ++t) {
+        const int u = lo + t;
+        if (u >= src.L) r[t] = 0;
+        b[t] = u / S;
+        s[t] = u % S;
+    }
+    const int twoK = 2 * K;
+    for (int j = 0; j < NB; ++j) {
+        int p[NW];
+#pragma unroll
+        for (int t = 0; t < NW; ++t) p[t] = (s[t] + (g * j * b[t]) % twoK) % twoK;
+        for (int c = 0; c < K; ++c) {
+            int acc = 0;
+#pragma unroll
+            for (int t = 0; t < NW; ++t) acc += p[t] == c ? r[t] : p[t] == c + K ? -r[t] : 0;
             constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
             store_digits<MODE>(out + ((size_t)(j * K + c) * PL) * nnp + e, nnp, acc);
         }
@@ -631,7 +729,7 @@ __global__ __launch_bounds__(256) void k_carry(const int64_t *__restrict__ Cw,
     }
 }
 
-// ---- fp32 decode (src/fpfixed.c:212-285) --------------------------------------
+// ---- fixed-point decode (src/fpfixed.c:212-322) ------------------------------
 // Carry over RL = 2L+2 limbs with an arithmetic shift, take the magnitude
 // (two's complement negation when the final carry is negative), keep the
 // top <= 4 limbs below the highest non-zero one plus a sticky bit, round to
@@ -661,11 +759,17 @@ struct TopTrack {
     }
 };
 
-__global__ __launch_bounds__(256) void k_decode_f32(const int64_t *__restrict__ Cw,
-                                                    float *__restrict__ out,
-                                                    size_t nn, int P, int RL,
-                                                    int SAB)
+// FMT: MFH_DEC_F32 rounds to 24 bits and writes fp32, MFH_DEC_F64 to 53
+// bits and fp64 (src/fpfixed.c:308-322), MFH_DEC_SIG63 to 63 bits and writes
+// the signed significand and the exponent of the long double decode
+// (src/fpfixed.c:292-306: int64 sig at out, int32 exponent at out2).
+template <int FMT>
+__global__ __launch_bounds__(256) void k_decode(const int64_t *__restrict__ Cw,
+                                                void *__restrict__ out_,
+                                                int32_t *__restrict__ out2,
+                                                size_t nn, int P, int RL, int SAB)
 {
+    constexpr int BITS = FMT == MFH_DEC_F32 ? 24 : FMT == MFH_DEC_F64 ? 53 : 63;
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= nn) return;
     TopTrack pos, neg;
@@ -684,7 +788,12 @@ __global__ __launch_bounds__(256) void k_decode_f32(const int64_t *__restrict__ 
     }
     const bool isneg = carry < 0;
     const int h = isneg ? neg.h : pos.h;
-    if (h < 0) { out[e] = 0.0f; return; }
+    if (h < 0) {
+        if constexpr (FMT == MFH_DEC_F32) ((float *)out_)[e] = 0.0f;
+        else if constexpr (FMT == MFH_DEC_F64) ((double *)out_)[e] = 0.0;
+        else { ((long long *)out_)[e] = 0; out2[e] = 0; }
+        return;
+    }
     uint32_t win[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) win[q] = isneg ? neg.win[q] : pos.win[q];
@@ -701,27 +810,46 @@ __global__ __launch_bounds__(256) void k_decode_f32(const int64_t *__restrict__ 
     int tb = 16 * h + bl - base;
     int shift = base;
     unsigned long long sig = top;
-    if (tb > 24) {
-        int drop = tb - 24;
+    // a window of at most BITS bits is returned as it stands (sticky unused)
+    if (tb > BITS) {
+        int drop = tb - BITS;
         sig = top >> drop;
         unsigned long long rem = top & ((1ULL << drop) - 1);
         unsigned long long half = 1ULL << (drop - 1);
         int up = rem > half ? 1 : rem < half ? 0 : (sticky ? 1 : (int)(sig & 1));
         sig += (unsigned long long)up;
-        if (sig >> 24) { sig >>= 1; drop++; }
+        if (sig >> BITS) { sig >>= 1; drop++; }
         shift += drop;
     }
-    float v = ldexpf((float)sig, shift - SAB);
-    out[e] = isneg ? -v : v;
+    if constexpr (FMT == MFH_DEC_F32) {
+        float v = ldexpf((float)sig, shift - SAB);
+        ((float *)out_)[e] = isneg ? -v : v;
+    } else if constexpr (FMT == MFH_DEC_F64) {
+        double v = ldexp((double)sig, shift - SAB);
+        ((double *)out_)[e] = isneg ? -v : v;
+    } else {
+        ((long long *)out_)[e] = isneg ? -(long long)sig : (long long)sig;
+        out2[e] = shift - SAB;
+    }
 }
 
-// ---- fp32 encode into limb planes (src/fpfixed.c:175-204) -------------------
-__global__ __launch_bounds__(256) void k_encode_f32(SrcF32 src, int32_t *__restrict__ out)
+// ---- fp32 / fp64 encode into limb planes (src/fpfixed.c:144-204) ------------
+// every one of the L planes is written (zero outside the entry's window)
+template <class Src>
+__global__ __launch_bounds__(256) void k_encode(Src src, int32_t *__restrict__ out)
 {
+    constexpr int NW = Src::NW;
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= src.nn) return;
     const int i = (int)(e / src.n), k = (int)(e % src.n);
-    for (int u = 0; u < src.L; ++u) out[(size_t)u * src.nn + e] = src.get(u, i, k);
+    int lo, r[NW];
+    src.window(i, k, lo, r);
+    for (int u = 0; u < src.L; ++u) {
+        int v = 0;
+#pragma unroll
+        for (int t = 0; t < NW; ++t) v = u == lo + t ? r[t] : v;
+        out[(size_t)u * src.nn + e] = v;
+    }
 }
 
 // ---- plane transpose (B operand) -----------------------------------------------
@@ -810,6 +938,9 @@ int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
     else if (elem_bytes == 4)
         hipLaunchKernelGGL(k_transpose<uint32_t>, grid, dim3(256), 0, st,
                            (const uint32_t *)src, (uint32_t *)dst, n);
+    else if (elem_bytes == 8)
+        hipLaunchKernelGGL(k_transpose<uint64_t>, grid, dim3(256), 0, st,
+                           (const uint64_t *)src, (uint64_t *)dst, n);
     else
         return MFH_E_ARG;
     MFH_HIP(hipGetLastError());
@@ -854,6 +985,17 @@ void launch_generic(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid, int LS)
                            s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
 }
 
+template <class Src>
+void launch_window(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid)
+{
+    if (c->mode == MFH_MODE_K7)
+        hipLaunchKernelGGL((k_forward_window<Src, MFH_MODE_K7>), grid, dim3(256), 0, c->stream,
+                           s, dst, c->np, c->S, c->NB, c->K, c->g);
+    else
+        hipLaunchKernelGGL((k_forward_window<Src, MFH_MODE_B8>), grid, dim3(256), 0, c->stream,
+                           s, dst, c->np, c->S, c->NB, c->K, c->g);
+}
+
 int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
                        int scale_S)
 {
@@ -893,7 +1035,12 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
     }
     case MFH_IN_F32: {
         SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
-        launch_generic<SrcF32>(c, s, dst, grid, LS);
+        launch_window<SrcF32>(c, s, dst, grid);
+        break;
+    }
+    case MFH_IN_F64: {
+        SrcF64 s{(const double *)src, nn, c->n, c->L, scale_S};
+        launch_window<SrcF64>(c, s, dst, grid);
         break;
     }
     default:
@@ -1004,22 +1151,38 @@ int mfh_launch_carry_planes(const int64_t *Cw, int P, size_t nn, uint16_t *out,
     return MFH_OK;
 }
 
-int mfh_launch_encode_f32(const float *X, int n, int L, int S, int32_t *out,
-                          hipStream_t st)
+int mfh_launch_encode(const void *X, int is_f64, int n, int L, int S, int32_t *out,
+                      hipStream_t st)
 {
     const size_t nn = (size_t)n * n;
-    SrcF32 s{X, nn, n, L, S};
-    hipLaunchKernelGGL(k_encode_f32, dim3((unsigned)((nn + 255) / 256)), dim3(256), 0, st,
-                       s, out);
+    const dim3 grid((unsigned)((nn + 255) / 256));
+    if (is_f64)
+        hipLaunchKernelGGL(k_encode<SrcF64>, grid, dim3(256), 0, st,
+                           SrcF64{(const double *)X, nn, n, L, S}, out);
+    else
+        hipLaunchKernelGGL(k_encode<SrcF32>, grid, dim3(256), 0, st,
+                           SrcF32{(const float *)X, nn, n, L, S}, out);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }
 
-int mfh_launch_decode_f32(mfh_ctx *c, const int64_t *Cw, int SAB, float *out)
+int mfh_launch_decode(mfh_ctx *c, const int64_t *Cw, int SAB, int fmt, void *out,
+                      int32_t *out2)
 {
     const size_t nn = (size_t)c->n * c->n;
-    hipLaunchKernelGGL(k_decode_f32, dim3((unsigned)((nn + 255) / 256)), dim3(256),
-                       0, c->stream, Cw, out, nn, 2 * c->L - 1, 2 * c->L + 2, SAB);
+    const dim3 grid((unsigned)((nn + 255) / 256));
+    const int P = 2 * c->L - 1, RL = 2 * c->L + 2;
+    if (fmt == MFH_DEC_F32)
+        hipLaunchKernelGGL(k_decode<MFH_DEC_F32>, grid, dim3(256), 0, c->stream, Cw, out,
+                           out2, nn, P, RL, SAB);
+    else if (fmt == MFH_DEC_F64)
+        hipLaunchKernelGGL(k_decode<MFH_DEC_F64>, grid, dim3(256), 0, c->stream, Cw, out,
+                           out2, nn, P, RL, SAB);
+    else if (fmt == MFH_DEC_SIG63 && out2)
+        hipLaunchKernelGGL(k_decode<MFH_DEC_SIG63>, grid, dim3(256), 0, c->stream, Cw, out,
+                           out2, nn, P, RL, SAB);
+    else
+        return MFH_E_ARG;
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }

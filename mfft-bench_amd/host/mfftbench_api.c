@@ -209,11 +209,39 @@ void conv_mfft(int64_t *Cw, const int32_t *A32, const int32_t *B32,
     if (rc) fail("conv_mfft", rc);
 }
 
+/* ---- schoolbook (src/kernel.c:1015-1033, src/methods.c:94-123) ---------- */
+void mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign, kernel_t k)
+{
+    t_last_error = 0;
+    if (k != KERNEL_HIP) { fail("mm_accum", MFH_E_UNSUPPORTED); return; }
+    int rc = mfh_mm_accum(C, A, B, n, sign);
+    if (rc) fail("mm_accum", rc);
+}
+
+void conv_limbplane(int64_t *Cw, const int32_t *A32, const int32_t *B32, int n, int L,
+                    kernel_t k)
+{
+    t_last_error = 0;
+    if (k != KERNEL_HIP) { fail("conv_limbplane", MFH_E_UNSUPPORTED); return; }
+    int rc = mfh_limbplane_conv(A32, B32, n, L, Cw);
+    if (rc) fail("conv_limbplane", rc);
+}
+
+void mm_limbplane(const uint16_t *Apl, const uint16_t *Bpl, int n, int L, kernel_t k,
+                  uint16_t *out, int RL)
+{
+    t_last_error = 0;
+    if (k != KERNEL_HIP) { fail("mm_limbplane", MFH_E_UNSUPPORTED); return; }
+    int rc = mfh_limbplane_mm(Apl, Bpl, n, L, out, RL);
+    if (rc) fail("mm_limbplane", rc);
+}
+
 /* ---- fp32 embedding (src/fpfixed.c) -------------------------------------- */
 static int next_pow2(int x) { int r = 1; while (r < x) r <<= 1; return r; }
 
-/* exponent range of finite nonzero entries: x = mi 2^e2, mi in [2^23, 2^24)
- * (src/fpfixed.c:40-54); host-side sizing, as in the reference */
+/* exponent range of finite nonzero entries: x = mi 2^e2 with mi an exact
+ * sig-bit integer (src/fpfixed.c:40-54, 115-129); host-side sizing, as in the
+ * reference */
 static void scan(const float *X, size_t nn, int *lo, int *hi, int *any)
 {
     int l = 1 << 30, h = -(1 << 30), seen = 0;
@@ -230,20 +258,37 @@ static void scan(const float *X, size_t nn, int *lo, int *hi, int *any)
     *lo = l; *hi = h; *any = seen;
 }
 
-typedef struct { const float *A, *B; } fpx_src;
+static void scan_d(const double *X, size_t nn, int *lo, int *hi, int *any)
+{
+    int l = 1 << 30, h = -(1 << 30), seen = 0;
+    for (size_t i = 0; i < nn; i++) {
+        double x = X[i];
+        if (x == 0.0 || !isfinite(x)) continue;
+        int e;
+        frexp(x, &e);
+        if (e - 53 < l) l = e - 53;
+        if (e - 53 > h) h = e - 53;
+        seen = 1;
+    }
+    if (!seen) { l = 0; h = 0; }
+    *lo = l; *hi = h; *any = seen;
+}
 
-int fpx_init(fpx_ctx *c, const float *A, const float *B, int n, int force_bits)
+/* the fp inputs given to fpx_encode / fpx_encode_d, for fpx_mm_f32/f64 */
+typedef struct { const void *A, *B; } fpx_src;
+
+/* grid and limb count (src/fpfixed.c:59-78): `sig` significand bits, `wr`
+ * limbs one shifted significand can touch; then the int64 guard and the host
+ * planes (src/fpfixed.c:80-94) */
+static int fpx_setup(fpx_ctx *c, int n, int loA, int hiA, int loB, int hiB,
+                     int anyA, int anyB, int sig, int wr, int force_bits)
 {
     size_t nn = (size_t)n * n;
-    int loA, hiA, loB, hiB, anyA, anyB;
-    scan(A, nn, &loA, &hiA, &anyA);
-    scan(B, nn, &loB, &hiB, &anyB);
     memset(c, 0, sizeof *c);
-    c->sig = 24;
+    c->sig = sig;
     c->spreadA = anyA ? hiA - loA : 0;
     c->spreadB = anyB ? hiB - loB : 0;
     int L;
-    /* src/fpfixed.c:59-78 */
     if (force_bits > 0) {
         c->SA = c->SB = force_bits / 2;
         L = next_pow2(force_bits / LIMB_BITS);
@@ -251,14 +296,13 @@ int fpx_init(fpx_ctx *c, const float *A, const float *B, int n, int force_bits)
         c->SA = -loA;
         c->SB = -loB;
         int spread = c->spreadA > c->spreadB ? c->spreadA : c->spreadB;
-        int bits = 24 + spread + 1;
+        int bits = sig + spread + 1;
         int need = (bits + LIMB_BITS - 1) / LIMB_BITS;
-        int need2 = spread / LIMB_BITS + 3;
+        int need2 = spread / LIMB_BITS + wr;
         L = next_pow2(need > need2 ? need : need2);
         if (L < 2) L = 2;
     }
     c->n = n; c->L = L;
-    /* src/fpfixed.c:84-88 */
     if ((double)n * L * 65535.0 * 65535.0 > 4.0e18) {
         fprintf(stderr, "fpx: n=%d L=%d would overflow int64 accumulators\n", n, L);
         t_last_error = MFH_E_BOUND;
@@ -271,16 +315,52 @@ int fpx_init(fpx_ctx *c, const float *A, const float *B, int n, int force_bits)
     return 0;
 }
 
-void fpx_encode(fpx_ctx *c, const float *A, const float *B)
+/* src/fpfixed.c:96-108: a 24-bit significand touches at most 3 limbs */
+int fpx_init(fpx_ctx *c, const float *A, const float *B, int n, int force_bits)
+{
+    size_t nn = (size_t)n * n;
+    int loA, hiA, loB, hiB, anyA, anyB;
+    scan(A, nn, &loA, &hiA, &anyA);
+    scan(B, nn, &loB, &hiB, &anyB);
+    return fpx_setup(c, n, loA, hiA, loB, hiB, anyA, anyB, 24, 3, force_bits);
+}
+
+/* src/fpfixed.c:131-142: a 53-bit significand touches at most 5 limbs */
+int fpx_init_d(fpx_ctx *c, const double *A, const double *B, int n, int force_bits)
+{
+    size_t nn = (size_t)n * n;
+    int loA, hiA, loB, hiB, anyA, anyB;
+    scan_d(A, nn, &loA, &hiA, &anyA);
+    scan_d(B, nn, &loB, &hiB, &anyB);
+    return fpx_setup(c, n, loA, hiA, loB, hiB, anyA, anyB, 53, 5, force_bits);
+}
+
+/* limb planes A32/B32 written on the device; the inputs are remembered for
+ * fpx_mm_f32 / fpx_mm_f64 */
+static void encode_common(fpx_ctx *c, const void *A, const void *B, int f64,
+                          const char *name)
 {
     double t0 = now_sec();
     t_last_error = 0;
-    int rc = mfh_fpx_encode(A, c->n, c->L, c->SA, c->A32);
-    if (!rc) rc = mfh_fpx_encode(B, c->n, c->L, c->SB, c->B32);
-    if (rc) { fail("fpx_encode", rc); return; }
+    int rc = f64 ? mfh_fpx_encode_f64(A, c->n, c->L, c->SA, c->A32)
+                 : mfh_fpx_encode(A, c->n, c->L, c->SA, c->A32);
+    if (!rc)
+        rc = f64 ? mfh_fpx_encode_f64(B, c->n, c->L, c->SB, c->B32)
+                 : mfh_fpx_encode(B, c->n, c->L, c->SB, c->B32);
+    if (rc) { fail(name, rc); return; }
     fpx_src *s = c->dev ? (fpx_src *)c->dev : calloc(1, sizeof(fpx_src));
     if (s) { s->A = A; s->B = B; c->dev = s; }
     c->enc_secs = now_sec() - t0;
+}
+
+void fpx_encode(fpx_ctx *c, const float *A, const float *B)
+{
+    encode_common(c, A, B, 0, "fpx_encode");
+}
+
+void fpx_encode_d(fpx_ctx *c, const double *A, const double *B)
+{
+    encode_common(c, A, B, 1, "fpx_encode_d");
 }
 
 void fpx_decode_f32(fpx_ctx *c, float *C)
@@ -292,18 +372,44 @@ void fpx_decode_f32(fpx_ctx *c, float *C)
     c->dec_secs = now_sec() - t0;
 }
 
-int fpx_mm_f32(fpx_ctx *c, const mfft_plan *p, float *C)
+void fpx_decode_f64(fpx_ctx *c, double *C)
 {
     t_last_error = 0;
-    fpx_src *s = (fpx_src *)c->dev;
-    if (!s || !p || !C) return fail("fpx_mm_f32", MFH_E_ARG);
+    int rc = mfh_fpx_decode_f64(c->Cw, c->n, c->L, c->SA + c->SB, C);
+    if (rc) fail("fpx_decode_f64", rc);
+}
+
+void fpx_decode_ld(fpx_ctx *c, long double *C)
+{
+    t_last_error = 0;
+    int rc = mfh_fpx_decode_ld(c->Cw, c->n, c->L, c->SA + c->SB, C);
+    if (rc) fail("fpx_decode_ld", rc);
+}
+
+static int fpx_mm_common(fpx_ctx *c, const mfft_plan *p, void *C, int f64, const char *name)
+{
+    t_last_error = 0;
+    fpx_src *s = c ? (fpx_src *)c->dev : NULL;
+    if (!s || !p || !C || (c->sig == 53) != (f64 != 0)) return fail(name, MFH_E_ARG);
     pthread_mutex_lock(&g_lock);
     mfh_ctx *h = NULL;
     int rc = get_ctx(c->n, c->L, p, &h);
-    if (!rc) rc = mfh_fpx_mm(h, s->A, s->B, c->SA, c->SB, C);
+    if (!rc)
+        rc = f64 ? mfh_fpx_mm_f64(h, s->A, s->B, c->SA, c->SB, C)
+                 : mfh_fpx_mm(h, s->A, s->B, c->SA, c->SB, C);
     pthread_mutex_unlock(&g_lock);
-    if (rc) return fail("fpx_mm_f32", rc);
+    if (rc) return fail(name, rc);
     return 0;
+}
+
+int fpx_mm_f32(fpx_ctx *c, const mfft_plan *p, float *C)
+{
+    return fpx_mm_common(c, p, C, 0, "fpx_mm_f32");
+}
+
+int fpx_mm_f64(fpx_ctx *c, const mfft_plan *p, double *C)
+{
+    return fpx_mm_common(c, p, C, 1, "fpx_mm_f64");
 }
 
 void fpx_free(fpx_ctx *c)

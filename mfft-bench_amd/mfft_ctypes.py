@@ -70,6 +70,22 @@ def load(path=None):
         "mfh_fpx_decode_dev": ([vp, vp, i, vp], i),
         "mfh_normalize": ([vp, i, i, vp, i], i), "mfh_fpx_encode": ([vp, i, i, i, vp], i),
         "mfh_fpx_decode": ([vp, i, i, i, vp], i),
+        "mfh_fpx_mm_f64_dev": ([vp, vp, vp, i, i, vp], i),
+        "mfh_fpx_mm_f64": ([vp, vp, vp, i, i, vp], i),
+        "mfh_fpx_decode_f64_dev": ([vp, vp, i, vp], i),
+        "mfh_fpx_encode_f64": ([vp, i, i, i, vp], i),
+        "mfh_fpx_decode_f64": ([vp, i, i, i, vp], i),
+        "mfh_fpx_decode_ld": ([vp, i, i, i, vp], i),
+        "mfh_fpx_decode_sig63": ([vp, i, i, i, vp, vp], i),
+        "mfh_mm_accum": ([vp, vp, vp, i, i], i),
+        "mfh_mm_accum_dev": ([vp, vp, vp, vp, i, i], i),
+        "mfh_limbplane_conv": ([vp, vp, i, i, vp], i),
+        "mfh_limbplane_conv_dev": ([vp, i, vp, vp, i, i, vp], i),
+        "mfh_limbplane_mm": ([vp, vp, i, i, vp, i], i),
+        "mfh_limbplane_mm_dev": ([vp, vp, vp, i, i, vp, vp, i], i),
+        "mm_accum": ([vp, vp, vp, i, i, i], None),
+        "mm_limbplane": ([vp, vp, i, i, i, vp, i], None),
+        "conv_limbplane": ([vp, vp, vp, i, i, i], None),
         "mfh_malloc": ([C.POINTER(vp), sz], i), "mfh_free": ([vp], i),
         "mfh_h2d": ([vp, vp, sz], i), "mfh_d2h": ([vp, vp, sz], i), "mfh_sync": ([vp], i),
         "mfh_rand_u16_dev": ([vp, vp, i, i, u64], i),
@@ -90,6 +106,11 @@ def load(path=None):
         "fpx_decode_f32": ([C.POINTER(FpxCtx), vp], None),
         "fpx_free": ([C.POINTER(FpxCtx)], None),
         "fpx_mm_f32": ([C.POINTER(FpxCtx), pl, vp], i),
+        "fpx_init_d": ([C.POINTER(FpxCtx), vp, vp, i, i], i),
+        "fpx_encode_d": ([C.POINTER(FpxCtx), vp, vp], None),
+        "fpx_decode_f64": ([C.POINTER(FpxCtx), vp], None),
+        "fpx_decode_ld": ([C.POINTER(FpxCtx), vp], None),
+        "fpx_mm_f64": ([C.POINTER(FpxCtx), pl, vp], i),
         "mfft_last_error": ([], i), "mfft_strerror": ([i], C.c_char_p),
         "kernel_name": ([i], C.c_char_p), "kernel_from_name": ([C.c_char_p], i),
         "now_sec": ([], C.c_double),
@@ -167,6 +188,11 @@ class Ctx:
     def fpx_mm(self, A, B, SA, SB):
         out = np.empty(self.n * self.n, dtype=np.float32)
         check(self.lib.mfh_fpx_mm(self.h, _p(A), _p(B), SA, SB, _p(out)), "mfh_fpx_mm")
+        return out
+
+    def fpx_mm_f64(self, A, B, SA, SB):
+        out = np.empty(self.n * self.n, dtype=np.float64)
+        check(self.lib.mfh_fpx_mm_f64(self.h, _p(A), _p(B), SA, SB, _p(out)), "mfh_fpx_mm_f64")
         return out
 
     # device-level helpers

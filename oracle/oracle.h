@@ -1,6 +1,6 @@
 /* oracle.h -- CPU restatement of hadilq/mfft-bench's exact-integer MFFT
  * matrix multiply (flat plan, packed int32->int64 leaf), its limb-plane and
- * textbook oracles, the fp32 fixed-point embedding, and checking helpers.
+ * textbook oracles, the fp32/fp64 fixed-point embedding, and checking helpers.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and
  * bench.py's cpu_baseline leg load this library, and only as the checker or
@@ -83,7 +83,7 @@ long long orc_mm_mfft_sampled(const uint16_t *Apl, const uint16_t *Bpl, int n,
                               int L, const orc_plan *p, uint16_t *out, int RL,
                               long long nprod_sample, double secs[4]);
 
-/* ---- fp32 fixed-point embedding (src/fpfixed.c) ------------------------- */
+/* ---- fp32/fp64 fixed-point embedding (src/fpfixed.c) ------------------- */
 typedef struct {
     int n, L;
     int SA, SB;
@@ -98,6 +98,14 @@ void orc_fpx_encode(orc_fpx *c, const float *A, const float *B);
 void orc_fpx_decode_f32(const orc_fpx *c, float *C);
 /* decode of a caller-provided Cw (2L-1 planes) with the context's scales */
 void orc_fpx_decode_f32_from(const orc_fpx *c, const int64_t *Cw, float *C);
+/* fp64 (src/fpfixed.c:115-173, 308-322) */
+int  orc_fpx_init_d(orc_fpx *c, const double *A, const double *B, int n,
+                    int force_bits);
+void orc_fpx_encode_d(orc_fpx *c, const double *A, const double *B);
+void orc_fpx_decode_f64_from(const orc_fpx *c, const int64_t *Cw, double *C);
+/* long double decode (src/fpfixed.c:292-306) as sig * 2^ex, |sig| < 2^63 */
+void orc_fpx_decode_sig63_from(const orc_fpx *c, const int64_t *Cw, int64_t *sig,
+                               int32_t *ex);
 void orc_fpx_free(orc_fpx *c);
 
 /* ---- checking helpers (not in the reference) ---------------------------- */

@@ -99,6 +99,10 @@ class Oracle:
         L.orc_fpx_decode_f32.argtypes = [C.POINTER(OrcFpx), vp]
         L.orc_fpx_decode_f32_from.argtypes = [C.POINTER(OrcFpx), vp, vp]
         L.orc_fpx_free.argtypes = [C.POINTER(OrcFpx)]
+        L.orc_fpx_init_d.argtypes = [C.POINTER(OrcFpx), vp, vp, i, i]
+        L.orc_fpx_encode_d.argtypes = [C.POINTER(OrcFpx), vp, vp]
+        L.orc_fpx_decode_f64_from.argtypes = [C.POINTER(OrcFpx), vp, vp]
+        L.orc_fpx_decode_sig63_from.argtypes = [C.POINTER(OrcFpx), vp, vp, vp]
         L.orc_fp32_rand.argtypes = [vp, C.c_size_t, u64, i, i]
         L.orc_entry_exact.argtypes = [vp, vp, i, i, i, i, i, vp, i]
         L.orc_freivalds.argtypes = [vp, vp, i, i, i, vp, i, i, u64]
@@ -176,6 +180,28 @@ class Oracle:
         self.lib.orc_fpx_encode(C.byref(ctx), _p(A), _p(B))
         return ctx
 
+    def fpx_d(self, A, B, n, force_bits):
+        """fp64 counterpart of fpx()"""
+        ctx = OrcFpx()
+        if self.lib.orc_fpx_init_d(C.byref(ctx), _p(A), _p(B), n, force_bits) != 0:
+            return None
+        self.lib.orc_fpx_encode_d(C.byref(ctx), _p(A), _p(B))
+        return ctx
+
+    def fpx_decode_f64_from(self, ctx, Cw):
+        out = np.empty(ctx.n * ctx.n, dtype=np.float64)
+        self.lib.orc_fpx_decode_f64_from(C.byref(ctx), _p(np.ascontiguousarray(Cw, np.int64)),
+                                         _p(out))
+        return out
+
+    def fpx_decode_sig63_from(self, ctx, Cw):
+        """long double decode as (sig, ex): value = sig * 2**ex"""
+        sig = np.empty(ctx.n * ctx.n, dtype=np.int64)
+        ex = np.empty(ctx.n * ctx.n, dtype=np.int32)
+        self.lib.orc_fpx_decode_sig63_from(C.byref(ctx), _p(np.ascontiguousarray(Cw, np.int64)),
+                                           _p(sig), _p(ex))
+        return sig, ex
+
     def fpx_planes(self, ctx):
         nn = ctx.n * ctx.n
         buf = lambda ptr, cnt, ct: np.ctypeslib.as_array(C.cast(ptr, C.POINTER(ct)), shape=(cnt,))
@@ -231,6 +257,10 @@ class Reference:
         L.fpx_encode.argtypes = [C.POINTER(RefFpx), vp, vp]
         L.fpx_decode_f32.argtypes = [C.POINTER(RefFpx), vp]
         L.fpx_free.argtypes = [C.POINTER(RefFpx)]
+        L.fpx_init_d.argtypes = [C.POINTER(RefFpx), vp, vp, i, i]
+        L.fpx_encode_d.argtypes = [C.POINTER(RefFpx), vp, vp]
+        L.fpx_decode_f64.argtypes = [C.POINTER(RefFpx), vp]
+        L.fpx_decode_ld.argtypes = [C.POINTER(RefFpx), vp]
 
     def bigmat_rand(self, n, L, seed):
         m = np.empty(L * n * n, dtype=np.uint16)
@@ -277,6 +307,30 @@ class Reference:
             cw = np.ctypeslib.as_array(C.cast(ctx.Cw, C.POINTER(C.c_int64)),
                                        shape=((2 * ctx.L - 1) * nn,)).copy()
             return out, ctx.L, ctx.SA, ctx.SB, cw
+        finally:
+            self.lib.fpx_free(C.byref(ctx))
+
+
+    def fpx_f64(self, A, B, n, force_bits):
+        """fp64 encode -> conv_limbplane (ikj leaf) -> decode_f64 and
+        decode_ld in the reference library.  Returns (C64, Cld, L, SA, SB,
+        A32, B32, Cw) with Cld as numpy longdouble."""
+        ctx = RefFpx()
+        if self.lib.fpx_init_d(C.byref(ctx), _p(A), _p(B), n, force_bits) != 0:
+            return None
+        try:
+            self.lib.fpx_encode_d(C.byref(ctx), _p(A), _p(B))
+            self.lib.conv_limbplane(ctx.Cw, ctx.A32, ctx.B32, n, ctx.L, 0)
+            out = np.empty(n * n, dtype=np.float64)
+            self.lib.fpx_decode_f64(C.byref(ctx), _p(out))
+            old = np.empty(n * n, dtype=np.longdouble)
+            self.lib.fpx_decode_ld(C.byref(ctx), _p(old))
+            nn = n * n
+            arr = lambda ptr, cnt, ct: np.ctypeslib.as_array(C.cast(ptr, C.POINTER(ct)),
+                                                             shape=(cnt,)).copy()
+            return (out, old, ctx.L, ctx.SA, ctx.SB, arr(ctx.A32, ctx.L * nn, C.c_int32),
+                    arr(ctx.B32, ctx.L * nn, C.c_int32),
+                    arr(ctx.Cw, (2 * ctx.L - 1) * nn, C.c_int64))
         finally:
             self.lib.fpx_free(C.byref(ctx))
 

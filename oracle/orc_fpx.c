@@ -1,11 +1,14 @@
-/* orc_fpx.c -- fp32 <-> fixed-point limb planes (src/fpfixed.c).
+/* orc_fpx.c -- fp32 / fp64 <-> fixed-point limb planes (src/fpfixed.c).
  * Test infrastructure only (see oracle.h).
  *
- * Every finite nonzero fp32 x is mi * 2^e2 with mi in [2^23, 2^24).  On a
- * grid of scale 2^S the integer x * 2^S is mi shifted left by e2 + S; that
- * shifted significand is written straight into (at most) three signed
- * base-2^16 limbs.  The exact product comes back at scale 2^(SA+SB) and is
- * rounded once, to nearest-even, to 24 significant bits. */
+ * Every finite nonzero fp32 x is mi * 2^e2 with mi in [2^23, 2^24) (fp64:
+ * [2^52, 2^53)).  On a grid of scale 2^S the integer x * 2^S is mi shifted
+ * left by e2 + S; that shifted significand is written straight into (at
+ * most) three (fp64: five) signed base-2^16 limbs.  The exact product comes
+ * back at scale 2^(SA+SB); the decoders gather the top <= 4 limbs of its
+ * magnitude and round that window to 24 / 53 / 63 bits, half-even with a
+ * sticky bit for everything below the window (a window that already has no
+ * more bits than that is kept as it is). */
 #include <stdlib.h>
 #include <string.h>
 #include <math.h>
@@ -30,6 +33,26 @@ static void exp_range(const float *X, size_t cnt, int *lo, int *hi, int *any)
     *lo = l; *hi = h; *any = seen;
 }
 
+/* src/fpfixed.c:115-129 */
+static void exp_range_d(const double *X, size_t cnt, int *lo, int *hi, int *any)
+{
+    int l = 1 << 30, h = -(1 << 30), seen = 0;
+    for (size_t i = 0; i < cnt; i++) {
+        double x = X[i];
+        if (x == 0.0 || !isfinite(x)) continue;
+        int e;
+        frexp(x, &e);
+        if (e - 53 < l) l = e - 53;
+        if (e - 53 > h) h = e - 53;
+        seen = 1;
+    }
+    if (!seen) { l = 0; h = 0; }
+    *lo = l; *hi = h; *any = seen;
+}
+
+static int setup(orc_fpx *c, int n, int loA, int hiA, int loB, int hiB,
+                 int anyA, int anyB, int sig, int wr, int force_bits);
+
 /* src/fpfixed.c:59-108 (fp32: 24-bit significand, touches <= 3 limbs). */
 int orc_fpx_init(orc_fpx *c, const float *A, const float *B, int n,
                  int force_bits)
@@ -38,6 +61,25 @@ int orc_fpx_init(orc_fpx *c, const float *A, const float *B, int n,
     int loA, hiA, loB, hiB, anyA, anyB;
     exp_range(A, nn, &loA, &hiA, &anyA);
     exp_range(B, nn, &loB, &hiB, &anyB);
+    return setup(c, n, loA, hiA, loB, hiB, anyA, anyB, 24, 3, force_bits);
+}
+
+/* src/fpfixed.c:131-142 (fp64: 53-bit significand, touches <= 5 limbs). */
+int orc_fpx_init_d(orc_fpx *c, const double *A, const double *B, int n,
+                   int force_bits)
+{
+    size_t nn = (size_t)n * n;
+    int loA, hiA, loB, hiB, anyA, anyB;
+    exp_range_d(A, nn, &loA, &hiA, &anyA);
+    exp_range_d(B, nn, &loB, &hiB, &anyB);
+    return setup(c, n, loA, hiA, loB, hiB, anyA, anyB, 53, 5, force_bits);
+}
+
+/* src/fpfixed.c:59-94 */
+static int setup(orc_fpx *c, int n, int loA, int hiA, int loB, int hiB,
+                 int anyA, int anyB, int sig, int wr, int force_bits)
+{
+    size_t nn = (size_t)n * n;
     memset(c, 0, sizeof *c);
     c->spreadA = anyA ? hiA - loA : 0;
     c->spreadB = anyB ? hiB - loB : 0;
@@ -48,10 +90,10 @@ int orc_fpx_init(orc_fpx *c, const float *A, const float *B, int n,
     } else {
         c->SA = -loA;
         c->SB = -loB;
-        int bits = 24 + (c->spreadA > c->spreadB ? c->spreadA : c->spreadB) + 1;
         int spread = c->spreadA > c->spreadB ? c->spreadA : c->spreadB;
+        int bits = sig + spread + 1;
         int need = (bits + ORC_LIMB_BITS - 1) / ORC_LIMB_BITS;
-        int need2 = spread / ORC_LIMB_BITS + 3;
+        int need2 = spread / ORC_LIMB_BITS + wr;
         L = next_pow2(need > need2 ? need : need2);
         if (L < 2) L = 2;
     }
@@ -82,6 +124,36 @@ static void encode_one(int32_t *planes, size_t nn, size_t idx, float x,
     int sgn = x < 0.0f ? -1 : 1;
     for (int t = 0; t < 3 && lo + t < L; t++)
         planes[(size_t)(lo + t) * nn + idx] = sgn * (int32_t)((v >> (16 * t)) & 0xFFFFu);
+}
+
+/* src/fpfixed.c:144-162: the 53-bit significand shifted by up to 15 bits
+ * needs 68 bits, kept as a (high, low) pair of 64-bit words */
+static void encode_one_d(int32_t *planes, size_t nn, size_t idx, double x,
+                         int L, int S)
+{
+    if (x == 0.0 || !isfinite(x)) return;
+    int e;
+    double m = frexp(x, &e);
+    uint64_t mi = (uint64_t)(fabs(m) * 9007199254740992.0);
+    int off = e - 53 + S;
+    if (off < 0) return;
+    int lo = off >> 4, sh = off & 15;
+    uint64_t w0 = mi << sh, w1 = sh ? mi >> (64 - sh) : 0;
+    int sgn = x < 0.0 ? -1 : 1;
+    for (int t = 0; t < 5 && lo + t < L; t++) {
+        uint64_t part = t < 4 ? w0 >> (16 * t) : w1;
+        planes[(size_t)(lo + t) * nn + idx] = sgn * (int32_t)(part & 0xFFFFu);
+    }
+}
+
+/* src/fpfixed.c:164-173 */
+void orc_fpx_encode_d(orc_fpx *c, const double *A, const double *B)
+{
+    size_t nn = (size_t)c->n * c->n;
+    memset(c->A32, 0, sizeof(int32_t) * (size_t)c->L * nn);
+    memset(c->B32, 0, sizeof(int32_t) * (size_t)c->L * nn);
+    for (size_t i = 0; i < nn; i++) encode_one_d(c->A32, nn, i, A[i], c->L, c->SA);
+    for (size_t i = 0; i < nn; i++) encode_one_d(c->B32, nn, i, B[i], c->L, c->SB);
 }
 
 void orc_fpx_encode(orc_fpx *c, const float *A, const float *B)
@@ -167,6 +239,43 @@ void orc_fpx_decode_f32_from(const orc_fpx *c, const int64_t *Cw, float *C)
 void orc_fpx_decode_f32(const orc_fpx *c, float *C)
 {
     orc_fpx_decode_f32_from(c, c->Cw, C);
+}
+
+/* src/fpfixed.c:308-322 */
+void orc_fpx_decode_f64_from(const orc_fpx *c, const int64_t *Cw, double *C)
+{
+    size_t nn = (size_t)c->n * c->n;
+    int32_t *limb = malloc(sizeof(int32_t) * (size_t)(2 * c->L + 2));
+    int S = c->SA + c->SB;
+    if (!limb) return;
+    for (size_t i = 0; i < nn; i++) {
+        uint64_t top; int tb, shift, sticky;
+        int sgn = extract(Cw, c->L, nn, i, limb, &top, &tb, &shift, &sticky);
+        if (!sgn) { C[i] = 0.0; continue; }
+        uint64_t sig = round_sig(top, tb, 53, sticky, &shift);
+        C[i] = (double)sgn * ldexp((double)sig, shift - S);
+    }
+    free(limb);
+}
+
+/* src/fpfixed.c:292-306, as a signed 63-bit significand and an exponent:
+ * the reference's long double is sig * 2^ex (exact in x87 extended) */
+void orc_fpx_decode_sig63_from(const orc_fpx *c, const int64_t *Cw, int64_t *sig,
+                               int32_t *ex)
+{
+    size_t nn = (size_t)c->n * c->n;
+    int32_t *limb = malloc(sizeof(int32_t) * (size_t)(2 * c->L + 2));
+    int S = c->SA + c->SB;
+    if (!limb) return;
+    for (size_t i = 0; i < nn; i++) {
+        uint64_t top; int tb, shift, sticky;
+        int sgn = extract(Cw, c->L, nn, i, limb, &top, &tb, &shift, &sticky);
+        if (!sgn) { sig[i] = 0; ex[i] = 0; continue; }
+        uint64_t s63 = round_sig(top, tb, 63, sticky, &shift);
+        sig[i] = sgn * (int64_t)s63;
+        ex[i] = shift - S;
+    }
+    free(limb);
 }
 
 /* src/fpfixed.c:324-328 */

@@ -14,11 +14,19 @@ the oracle and of the reference code:
   2^(16 RL).
 * fpx.json -- the fp32 embedding (src/fpfixed.c): the exact product of two
   fp32 matrices rounded once to binary32, round-half-even, +0.0 for zero.
+* fpx64.json -- the fp64 embedding (src/fpfixed.c:115-173, 292-322).  With V
+  the exact product scaled onto the integer grid, the reference keeps the
+  window of |V|'s top <= 4 base-2^16 limbs; a window wider than the target
+  precision (53 bits for fp64, 63 for long double) is rounded to nearest,
+  ties to even, on the exact value (Python's float(Fraction) for fp64), and
+  a narrower window is returned as it stands, dropping what lies below it.
+  Long double results are written as (sig, ex) with value sig * 2^ex.
 * splitmix.json -- the first outputs of SplitMix64 for two seeds.
 
 Run from the repository root:  python tests/golden/gen_golden.py
 """
 import json
+import math
 import os
 import struct
 from fractions import Fraction
@@ -143,6 +151,104 @@ def fpx_case(n, seed_a, seed_b, emin, emax):
             "C_bits": bits}
 
 
+def f64_bits(x):
+    return struct.unpack("<Q", struct.pack("<d", x))[0]
+
+
+def fp64_rand(count, seed, emin, emax):
+    """+-m 2^e with m = 1 + (low 52 bits of u) / 2^52, e = emin + u mod span,
+    sign = top bit of u (one splitmix64 draw per value)"""
+    g = splitmix(seed)
+    xs = []
+    for _ in range(count):
+        u = next(g)
+        m = 1.0 + (u & ((1 << 52) - 1)) / float(1 << 52)
+        x = m * 2.0 ** (emin + u % (emax - emin + 1))
+        xs.append(-x if u >> 63 else x)
+    return xs
+
+
+def window_decode(q, S, bits):
+    """The reference's decode of the exact rational q = C[i][j] on a grid of
+    scale 2^S, as (sign, sig, ex) with value sign * sig * 2^ex."""
+    V = q * Fraction(2) ** S
+    assert V.denominator == 1
+    V = V.numerator
+    if V == 0:
+        return 1, 0, 0, True
+    sign = -1 if V < 0 else 1
+    V = abs(V)
+    blen = V.bit_length()
+    h = (blen - 1) // 16                 # top non-zero limb
+    k = min(h + 1, 4)
+    base = 16 * (h - k + 1)
+    tb = blen - base                     # bits in the window
+    if tb <= bits:
+        return sign, V >> base, base - S, True
+    drop = blen - bits
+    sig = round(Fraction(V, 1 << drop))  # half-even on the exact value
+    if sig >> bits:
+        sig >>= 1
+        drop += 1
+    return sign, sig, drop - S, False
+
+
+def fpx64_case(A, B, n, force_bits, name):
+    C64, sig, ex, trunc = [], [], [], 0
+    for i in range(n):
+        for j in range(n):
+            q = sum(Fraction(A[i * n + k]) * Fraction(B[k * n + j]) for k in range(n))
+            # the window's limbs are those of q 2^(SA+SB)
+            sg, s53, e53, narrow = window_decode(q, S_of(A, B, n, force_bits), 53)
+            v = sg * math.ldexp(float(s53), e53) if s53 else 0.0
+            if not narrow and abs(v) >= 2.0 ** -1022:
+                assert v == float(q)          # round to nearest, ties to even
+            if narrow and Fraction(s53) * Fraction(2) ** e53 != abs(q):
+                trunc += 1
+            C64.append(f64_bits(v))
+            sg, s63, e63, _ = window_decode(q, S_of(A, B, n, force_bits), 63)
+            sig.append(sg * s63)
+            ex.append(e63)
+    return {"name": name, "n": n, "force_bits": force_bits,
+            "A_bits": [f64_bits(a) for a in A], "B_bits": [f64_bits(b) for b in B],
+            "C64_bits": C64, "ld_sig": sig, "ld_ex": ex, "truncated_f64": trunc}
+
+
+def S_of(A, B, n, force_bits):
+    """SA + SB of the grid (src/fpfixed.c:59-71): force_bits/2 each, or minus
+    the smallest exponent of the matrix's entries written as mi 2^e2 with mi
+    a 53-bit integer"""
+    if force_bits:
+        return force_bits
+    def lo(X):
+        es = [math.frexp(x)[1] - 53 for x in X if x != 0.0]
+        return min(es) if es else 0
+    return -lo(A) - lo(B)
+
+
+def fpx64_edges():
+    """Hand-made entries, n = 4 (data-sized grid, every entry on it).  B's
+    columns pick: row sums, A[i][0] + 3 A[i][1], A[i][2] / 2, nothing.
+      C[0][0] = 64 + 2^-47 + 2^-70: a 49-bit window; what lies below it
+                (more than half an ulp) is dropped: 64, where rounding to
+                nearest would give 64 + 2^-46
+      C[1][0] = 1 + 2^-53 (tie, even: 1);  C[1][1] = 1 + 3 2^-53 (tie, odd:
+                1 + 2^-51);  C[3][0] = -(1 + 2^-53 + 2^-80) (past the tie:
+                -(1 + 2^-52));  C[3][1] = -(1 + 3 2^-53) (-(1 + 2^-51))
+      C[2][1] = -4.5 + 4.5: exact zero, +0.0;  C[2][2] = 1.5 2^-1074: the
+                subnormal result rounds (ties to even) to 2^-1073"""
+    t = 2.0 ** -1074
+    A = [64.0, 2.0 ** -47, 2.0 ** -70, 0.0,
+         1.0, 2.0 ** -53, 0.0, 0.0,
+         -4.5, 1.5, 3 * t, 0.0,
+         -1.0, -(2.0 ** -53), 0.0, -(2.0 ** -80)]
+    B = [1.0, 1.0, 0.0, 0.0,
+         1.0, 3.0, 0.0, 0.0,
+         1.0, 0.0, 0.5, 0.0,
+         1.0, 0.0, 0.0, 0.0]
+    return A, B
+
+
 def main():
     seed = 12345
     products = []
@@ -152,10 +258,16 @@ def main():
         products.append(product_case(n, L, seed + 1, (seed + 1) ^ 0xABCDEF, True))
     normalize = [normalize_case(3, 5, 8, 99), normalize_case(4, 7, 15, 7)]
     fpx = [fpx_case(3, 11, 22, -20, 20), fpx_case(6, 33, 44, -20, 20), fpx_case(4, 55, 66, -3, 3)]
+    fpx64 = [fpx64_case(fp64_rand(9, 71, -20, 20), fp64_rand(9, 72, -20, 20), 3, 0, "rand3"),
+             fpx64_case(fp64_rand(16, 73, -30, 30), fp64_rand(16, 74, -30, 30), 4, 2048,
+                        "rand4_grid2048"),
+             fpx64_case(fp64_rand(25, 75, -300, 300), fp64_rand(25, 76, -300, 300), 5, 0,
+                        "rand5_wide"),
+             fpx64_case(*fpx64_edges(), 4, 0, "edges")]
     g0, g1 = splitmix(0), splitmix(12345)
     sm = {"seed0": [next(g0) for _ in range(4)], "seed12345": [next(g1) for _ in range(4)]}
     for name, obj in [("products", products), ("normalize", normalize), ("fpx", fpx),
-                      ("splitmix", sm)]:
+                      ("fpx64", fpx64), ("splitmix", sm)]:
         with open(os.path.join(HERE, f"{name}.json"), "w") as f:
             json.dump(obj, f, separators=(",", ":"))
         print("wrote", name)

@@ -133,8 +133,39 @@ def test_fpx_init_sizing_matches_reference_rules(lib, orc):
                (oc.L, oc.SA, oc.SB, oc.spreadA, oc.spreadB)
         lib.fpx_free(C.byref(ctx))
         orc.fpx_free(oc)
+    # fp64 sizing (src/fpfixed.c:131-142): 53-bit significands, 5-limb reach
+    Ad = A.astype(np.float64) * 2.0 ** -700
+    Bd = B.astype(np.float64) * (1.0 + 2.0 ** -40)
+    for force in (2048, 0):
+        ctx = M.FpxCtx()
+        assert lib.fpx_init_d(C.byref(ctx), Ad.ctypes.data, Bd.ctypes.data, n, force) == 0
+        oc = orc.fpx_d(Ad, Bd, n, force)
+        assert (ctx.L, ctx.SA, ctx.SB, ctx.spreadA, ctx.spreadB, ctx.sig) == \
+               (oc.L, oc.SA, oc.SB, oc.spreadA, oc.spreadB, 53)
+        lib.fpx_free(C.byref(ctx))
+        orc.fpx_free(oc)
     # src/fpfixed.c:84-88 overflow guard
     nb = 1024                                   # n * L * 65535^2 > 4e18 at L = 2^20
     big = np.ones(nb * nb, np.float32)
     ctx = M.FpxCtx()
     assert lib.fpx_init(C.byref(ctx), big.ctypes.data, big.ctypes.data, nb, 1 << 24) == -1
+
+
+def test_schoolbook_rejects_cpu_leaves_and_leaves_outputs_untouched(lib):
+    """mm_accum / conv_limbplane / mm_limbplane with a CPU kernel_t: error
+    code, message, outputs untouched (no device call is made)."""
+    import mfft_ctypes as M
+    n, L = 4, 2
+    A = np.ones(n * n, np.int32)
+    Cm = np.full(n * n, 7, np.int64)
+    lib.mm_accum(Cm.ctypes.data, A.ctypes.data, A.ctypes.data, n, 1, M.KERNEL_PACKED)
+    assert lib.mfft_last_error() == -7 and np.all(Cm == 7)
+    Cw = np.full((2 * L - 1) * n * n, 7, np.int64)
+    A32 = np.ones(L * n * n, np.int32)
+    lib.conv_limbplane(Cw.ctypes.data, A32.ctypes.data, A32.ctypes.data, n, L, M.KERNEL_IKJ)
+    assert lib.mfft_last_error() == -7 and np.all(Cw == 7)
+    A16 = np.ones(L * n * n, np.uint16)
+    out = np.full((2 * L + 1) * n * n, 7, np.uint16)
+    lib.mm_limbplane(A16.ctypes.data, A16.ctypes.data, n, L, M.KERNEL_PACKED, out.ctypes.data,
+                     2 * L + 1)
+    assert lib.mfft_last_error() == -7 and np.all(out == 7)

@@ -1,5 +1,6 @@
 """GPU parity of every entry point, through the C-ABI: conv_mfft on signed
-limbs, two's complement products, the fp32 embedding, device normalize /
+limbs, two's complement products, the fp32 and fp64 embeddings and the long
+double decode, device normalize /
 encode / decode, the device input generator, the generic (runtime-plan)
 kernels, and the full-size workloads checked by Freivalds' test plus exact
 sampled entries."""
@@ -228,6 +229,82 @@ def test_fpx_zero_and_signs(gpu, orc, lib):
     orc.fpx_free(oc)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     assert np.all(got[:n].view(np.uint32) == 0)           # +0.0f
+
+
+# ---- fp64 embedding and the long double decode -------------------------------------
+def host_view(ptr, count, ctype):
+    return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(ctype)), shape=(count,))
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_fpx64_fixture(gpu, orc, lib, case):
+    """fpx_init_d / fpx_encode_d / conv_mfft / fpx_decode_f64 / fpx_decode_ld
+    and the fused fpx_mm_f64 against the Fraction fixtures (fpx64.json)."""
+    with open(os.path.join(GOLD, "fpx64.json")) as f:
+        c = json.load(f)[case]
+    n, force = c["n"], c["force_bits"]
+    print(f"[fpx64] {c['name']} n={n}", flush=True)
+    A = np.array(c["A_bits"], dtype=np.uint64).view(np.float64)
+    B = np.array(c["B_bits"], dtype=np.uint64).view(np.float64)
+    want = np.array(c["C64_bits"], dtype=np.uint64)
+    ctx = gpu.FpxCtx()
+    assert lib.fpx_init_d(C.byref(ctx), A.ctypes.data, B.ctypes.data, n, force) == 0
+    assert ctx.sig == 53
+    lib.fpx_encode_d(C.byref(ctx), A.ctypes.data, B.ctypes.data)
+    assert lib.mfft_last_error() == 0
+    p = gpu.plan(ctx.L)
+    out = np.empty(n * n, np.float64)
+    assert lib.fpx_mm_f64(C.byref(ctx), C.byref(p), out.ctypes.data) == 0
+    assert np.array_equal(out.view(np.uint64), want)
+    nn = n * n
+    oc = orc.fpx_d(A, B, n, force)
+    oa, ob = orc.fpx_planes(oc)
+    orc.fpx_free(oc)
+    assert np.array_equal(host_view(ctx.A32, ctx.L * nn, C.c_int32), oa)   # device encode
+    assert np.array_equal(host_view(ctx.B32, ctx.L * nn, C.c_int32), ob)
+    lib.conv_mfft(ctx.Cw, ctx.A32, ctx.B32, n, ctx.L, C.byref(p), gpu.KERNEL_HIP)
+    assert lib.mfft_last_error() == 0
+    out2 = np.empty(n * n, np.float64)
+    lib.fpx_decode_f64(C.byref(ctx), out2.ctypes.data)
+    assert np.array_equal(out2.view(np.uint64), want)
+    ld = np.empty(n * n, np.longdouble)
+    lib.fpx_decode_ld(C.byref(ctx), ld.ctypes.data)
+    assert lib.mfft_last_error() == 0
+    want_ld = np.ldexp(np.array(c["ld_sig"], dtype=np.int64).astype(np.longdouble),
+                       np.array(c["ld_ex"], dtype=np.int32))
+    assert np.array_equal(ld, want_ld)
+    lib.fpx_free(C.byref(ctx))
+
+
+@pytest.mark.parametrize("n,force,emin,emax", [(64, 2048, -60, 60), (96, 0, -100, 100),
+                                               (128, 0, -8, 8)])
+def test_fpx64_random(gpu, orc, lib, n, force, emin, emax):
+    """fpx_mm_f64 (device encode, product, decode) and the sig/exponent
+    decode against the oracle on random fp64 matrices, padded and unpadded
+    sizes, fixed and data-sized grids."""
+    print(f"[fpx64] n={n} force={force}", flush=True)
+    rng = np.random.default_rng(n + force)
+    A = np.ldexp(rng.uniform(1, 2, n * n) * rng.choice([-1, 1], n * n),
+                 rng.integers(emin, emax + 1, n * n))
+    B = np.ldexp(rng.uniform(1, 2, n * n) * rng.choice([-1, 1], n * n),
+                 rng.integers(emin, emax + 1, n * n))
+    A[:n] = 0.0                                           # row 0 of C: +0.0
+    oc = orc.fpx_d(A, B, n, force)
+    oa, ob = orc.fpx_planes(oc)
+    L, SA, SB = oc.L, oc.SA, oc.SB
+    cw = orc.conv_mfft(oa, ob, n, L, orc.plan(L))
+    want = orc.fpx_decode_f64_from(oc, cw)
+    sig, ex = orc.fpx_decode_sig63_from(oc, cw)
+    orc.fpx_free(oc)
+    with gpu.Ctx(n, L) as ctx:
+        got = ctx.fpx_mm_f64(A, B, SA, SB)
+    assert np.array_equal(got.view(np.uint64), want.view(np.uint64))
+    assert np.all(got[:n].view(np.uint64) == 0)
+    dsig = np.empty(n * n, np.int64)
+    dex = np.empty(n * n, np.int32)
+    gpu.check(lib.mfh_fpx_decode_sig63(cw.ctypes.data, n, L, SA + SB, dsig.ctypes.data,
+                                       dex.ctypes.data))
+    assert np.array_equal(dsig, sig) and np.array_equal(dex, ex)
 
 
 # ---- full-size workloads ------------------------------------------------------------------

@@ -1,0 +1,120 @@
+"""GPU parity of the schoolbook entry points through the C-ABI: the leaf
+operator mm_accum (exact modulo 2^64 for any int32 entries), conv_limbplane
+and mm_limbplane, against Python integers, the oracle and the golden
+products; and the MFFT product checked against the schoolbook at the
+n=1024, 2048-bit workload on the device."""
+import ctypes as C
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+SEED, SEED_B = 12345, 12345 ^ 0xABCDEF
+M64 = (1 << 64) - 1
+
+
+def exact_mm_mod64(C0, A, B, n, sign):
+    """C0 +/- A B over Python integers, reduced to int64 two's complement."""
+    P = A.reshape(n, n).astype(object).dot(B.reshape(n, n).astype(object))
+    out = []
+    for c, p in zip(C0.tolist(), P.reshape(-1).tolist()):
+        v = (c + p if sign > 0 else c - p) & M64
+        out.append(v - (1 << 64) if v >> 63 else v)
+    return np.array(out, dtype=np.int64)
+
+
+@pytest.mark.parametrize("n,sign", [(1, 1), (7, -1), (64, 1), (100, 0), (130, 1)])
+def test_mm_accum_full_int32_range(gpu, lib, n, sign):
+    rng = np.random.default_rng(n)
+    A = rng.integers(-2 ** 31, 2 ** 31, size=n * n, dtype=np.int64).astype(np.int32)
+    B = rng.integers(-2 ** 31, 2 ** 31, size=n * n, dtype=np.int64).astype(np.int32)
+    A[0], B[0] = -2 ** 31, -2 ** 31                      # the one product of 2^62
+    C0 = rng.integers(-2 ** 63, 2 ** 63 - 1, size=n * n, dtype=np.int64)
+    want = exact_mm_mod64(C0, A, B, n, sign)
+    got = C0.copy()
+    lib.mm_accum(got.ctypes.data, A.ctypes.data, B.ctypes.data, n, sign, gpu.KERNEL_HIP)
+    assert lib.mfft_last_error() == 0
+    assert np.array_equal(got, want)
+
+
+def test_mm_accum_matches_oracle_leaf(gpu, orc, lib):
+    n = 192
+    rng = np.random.default_rng(5)
+    A = rng.integers(-65535, 65536, size=n * n).astype(np.int32)
+    B = rng.integers(-65535, 65536, size=n * n).astype(np.int32)
+    want = np.zeros(n * n, np.int64)
+    orc.mm_accum(want, A, B, n, 1)
+    orc.mm_accum(want, B, A, n, -1)
+    got = np.zeros(n * n, np.int64)
+    gpu.check(lib.mfh_mm_accum(got.ctypes.data, A.ctypes.data, B.ctypes.data, n, 1))
+    gpu.check(lib.mfh_mm_accum(got.ctypes.data, B.ctypes.data, A.ctypes.data, n, -1))
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("n,L", [(5, 2), (16, 8), (33, 16), (64, 32), (20, 128)])
+def test_conv_limbplane(gpu, orc, lib, n, L):
+    print(f"[conv_limbplane] n={n} L={L}", flush=True)
+    rng = np.random.default_rng(n * L)
+    A = rng.integers(-65535, 65536, size=L * n * n).astype(np.int32)
+    B = rng.integers(-65535, 65536, size=L * n * n).astype(np.int32)
+    A[:7] = 2 ** 31 - 1                                  # outside the MFFT's limb range
+    B[:7] = -2 ** 31
+    want = orc.conv_limbplane(A, B, n, L)
+    cw = np.zeros((2 * L - 1) * n * n, np.int64)
+    lib.conv_limbplane(cw.ctypes.data, A.ctypes.data, B.ctypes.data, n, L, gpu.KERNEL_HIP)
+    assert lib.mfft_last_error() == 0
+    assert np.array_equal(cw, want)
+
+
+def test_mm_limbplane_golden_products(gpu, orc, lib):
+    with open(os.path.join(GOLD, "products.json")) as f:
+        cases = [c for c in json.load(f) if not c["signed"]]
+    assert cases
+    for c in cases:
+        n, L, RL = c["n"], c["L"], c["RL"]
+        A = orc.bigmat_rand(n, L, c["seed_a"])       # the fixture's seeded inputs
+        B = orc.bigmat_rand(n, L, c["seed_b"])
+        out = np.zeros(RL * n * n, np.uint16)
+        lib.mm_limbplane(A.ctypes.data, B.ctypes.data, n, L, gpu.KERNEL_HIP, out.ctypes.data, RL)
+        assert lib.mfft_last_error() == 0
+        assert np.array_equal(out, np.array(c["out"], dtype=np.uint16)), (n, L)
+
+
+@pytest.mark.parametrize("n,L", [(48, 64), (64, 128)])
+def test_mm_limbplane_matches_oracle(gpu, orc, lib, n, L):
+    A = orc.bigmat_rand(n, L, SEED)
+    B = orc.bigmat_rand(n, L, SEED_B)
+    RL = 2 * L + 1
+    out = np.zeros(RL * n * n, np.uint16)
+    lib.mm_limbplane(A.ctypes.data, B.ctypes.data, n, L, gpu.KERNEL_HIP, out.ctypes.data, RL)
+    assert lib.mfft_last_error() == 0
+    assert np.array_equal(out, orc.mm_limbplane(A, B, n, L, RL))
+
+
+def test_mfft_equals_schoolbook_n1024_w2048(gpu, orc, lib):
+    """The headline product computed twice on the device, by the MFFT path
+    (int8 MFMA) and by the integer-ALU schoolbook, limb for limb."""
+    n, L = 1024, 128
+    RL = 2 * L + 1
+    print("[schoolbook] n=1024 W=2048", flush=True)
+    with gpu.Ctx(n, L) as ctx:
+        dA, dB = gpu.DevBuf(L * n * n * 2), gpu.DevBuf(L * n * n * 2)
+        dO1, dO2 = gpu.DevBuf(RL * n * n * 2), gpu.DevBuf(RL * n * n * 2)
+        dCw = gpu.DevBuf((2 * L - 1) * n * n * 8)
+        gpu.check(lib.mfh_rand_u16_dev(ctx.h, dA.ptr, n, L, SEED))
+        gpu.check(lib.mfh_rand_u16_dev(ctx.h, dB.ptr, n, L, SEED_B))
+        gpu.check(lib.mfh_mm_dev(ctx.h, gpu.MFH_IN_U16, dA.ptr, dB.ptr, dO1.ptr, RL))
+        gpu.check(lib.mfh_limbplane_mm_dev(ctx.h, dA.ptr, dB.ptr, n, L, dCw.ptr, dO2.ptr, RL))
+        ctx.sync()
+        o1 = dO1.download(np.uint16, RL * n * n)
+        o2 = dO2.download(np.uint16, RL * n * n)
+        for b in (dA, dB, dO1, dO2, dCw):
+            b.free()
+    assert np.array_equal(o1, o2)
+    A = orc.bigmat_rand(n, L, SEED)
+    B = orc.bigmat_rand(n, L, SEED_B)
+    assert orc.freivalds(A, B, n, L, o2, RL, nprimes=1)

@@ -314,3 +314,81 @@ def test_roots_post_arrays_and_order():
             if k == K:
                 assert np.array_equal(P, -np.eye(K, dtype=np.int64))   # I^K = -1
         assert np.array_equal(P, np.eye(K, dtype=np.int64))            # order 2K
+
+
+# ---- fp64 embedding and the long double decode ---------------------------------
+def bits_to_f64(bits):
+    return np.array(bits, dtype=np.uint64).view(np.float64)
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_fpx64_fixture(orc, case):
+    """Encode, exact product and decode against Fraction arithmetic: rounding
+    to nearest-even where the top 4-limb window is wider than the target,
+    the window as it stands where it is not (fpx64.json)."""
+    c = load("fpx64.json")[case]
+    n = c["n"]
+    A, B = bits_to_f64(c["A_bits"]), bits_to_f64(c["B_bits"])
+    ctx = orc.fpx_d(A, B, n, c["force_bits"])
+    A32, B32 = orc.fpx_planes(ctx)
+    cw = orc.conv_limbplane(A32, B32, n, ctx.L)
+    got = orc.fpx_decode_f64_from(ctx, cw)
+    sig, ex = orc.fpx_decode_sig63_from(ctx, cw)
+    orc.fpx_free(ctx)
+    assert np.array_equal(got.view(np.uint64), np.array(c["C64_bits"], dtype=np.uint64))
+    assert sig.tolist() == c["ld_sig"] and ex.tolist() == c["ld_ex"]
+
+
+def test_fpx64_fixture_covers_both_regimes():
+    cases = load("fpx64.json")
+    assert all(c["truncated_f64"] > 0 for c in cases)
+    edges = next(c for c in cases if c["name"] == "edges")
+    C64 = bits_to_f64(edges["C64_bits"]).reshape(4, 4)
+    assert C64[0, 0] == 64.0                       # window kept: not 64 + 2^-46
+    assert C64[1, 0] == 1.0 and C64[1, 1] == 1.0 + 2.0 ** -51    # ties: even, up
+    assert C64[3, 0] == -(1.0 + 2.0 ** -52) and C64[3, 1] == -(1.0 + 2.0 ** -51)
+    assert C64[2, 2] == 2.0 ** -1073               # subnormal, ties to even
+    assert np.all(C64[:, 3].view(np.uint64) == 0) and C64[2, 1].view(np.uint64) == 0
+
+
+def test_fpx64_encode_limbs_sum_to_value(orc):
+    """sum_u A32[u] 2^(16u) == x 2^SA exactly, for every entry on the grid."""
+    from fractions import Fraction
+    n = 5
+    rng = np.random.default_rng(3)
+    A = (rng.standard_normal(n * n) * 2.0 ** rng.integers(-40, 40, n * n)).astype(np.float64)
+    A[3] = 0.0
+    A[7] = -A[7]
+    ctx = orc.fpx_d(A, A, n, 0)
+    A32, _ = orc.fpx_planes(ctx)
+    L, SA = ctx.L, ctx.SA
+    orc.fpx_free(ctx)
+    planes = A32.reshape(L, n * n)
+    for e in range(n * n):
+        v = sum(int(planes[u, e]) << (16 * u) for u in range(L))
+        assert Fraction(v) == Fraction(float(A[e])) * Fraction(2) ** SA
+        assert np.all(np.abs(planes[:, e]) <= 65535)
+        assert np.count_nonzero(planes[:, e]) <= 5
+
+
+def test_fpx64_matches_reference(orc, ref):
+    for n, force, emin, emax in [(6, 0, -20, 20), (5, 2048, -60, 60), (4, 0, -500, 500)]:
+        rng = np.random.default_rng(n + force)
+        A = np.ldexp(rng.uniform(1, 2, n * n) * rng.choice([-1, 1], n * n),
+                     rng.integers(emin, emax + 1, n * n))
+        B = np.ldexp(rng.uniform(1, 2, n * n) * rng.choice([-1, 1], n * n),
+                     rng.integers(emin, emax + 1, n * n))
+        A[0] = 0.0
+        want64, want_ld, L, SA, SB, rA, rB, rcw = ref.fpx_f64(A, B, n, force)
+        ctx = orc.fpx_d(A, B, n, force)
+        assert (ctx.L, ctx.SA, ctx.SB) == (L, SA, SB)
+        A32, B32 = orc.fpx_planes(ctx)
+        assert np.array_equal(A32, rA) and np.array_equal(B32, rB)
+        cw = orc.conv_limbplane(A32, B32, n, L)
+        assert np.array_equal(cw, rcw)
+        got = orc.fpx_decode_f64_from(ctx, cw)
+        sig, ex = orc.fpx_decode_sig63_from(ctx, cw)
+        orc.fpx_free(ctx)
+        assert np.array_equal(got.view(np.uint64), want64.view(np.uint64))
+        ld = np.ldexp(sig.astype(np.longdouble), ex)
+        assert np.array_equal(ld, want_ld)
