@@ -136,6 +136,11 @@ int mfh_limbplane_mm(const uint16_t *A, const uint16_t *B, int n, int L, uint16_
 int mfh_limbplane_mm_dev(mfh_ctx *ctx, const void *dA, const void *dB, int n, int L,
                          void *dCw, void *dOut, int RL);
 
+/* negacyclic convolution C = A*B mod (t^K + 1) of K int32 planes into K
+ * int64 planes (ssa_negconv, src/mfft.c:560-662): the limb-plane
+ * convolution folded by t^K = -1 */
+int mfh_negconv(const int32_t *A, const int32_t *B, int K, int n, int64_t *C);
+
 /* ---- device memory and timing helpers ----------------------------------- */
 int  mfh_malloc(void **dptr, size_t bytes);
 int  mfh_free(void *dptr);

@@ -80,6 +80,15 @@ typedef struct {
 } mfft_plan;
 
 int       mfft_plan_init(mfft_plan *p, int L, int sigma_override);
+/* src/mfftbench.h:149, src/mfft.c:664-686: the plan whose pointwise step is
+ * a recursive negacyclic convolution (rec = 1, nprod = the reference's
+ * product count).  mm_mfft / conv_mfft accept it: the device runs its outer
+ * transform and does the pointwise products on the matrix cores. */
+int       mfft_plan_init_rec(mfft_plan *p, int L, int n, int sigma_override);
+/* src/mfftbench.h:150-151, src/mfft.c:560-662: negacyclic convolution of K
+ * int32 n x n planes into K int64 planes (k must be KERNEL_HIP) */
+void      ssa_negconv(int64_t *C, const int32_t *A, const int32_t *B, int K, int n,
+                      int Mbits, kernel_t k);
 long long mfft_plan_products(const mfft_plan *p);
 double    mfft_plan_maxbits(const mfft_plan *p, int n);
 void      mfft_plan_describe(const mfft_plan *p, int n);

@@ -126,7 +126,30 @@ __global__ __launch_bounds__(256) void k_conv_limbplane(long long *__restrict__ 
         }
 }
 
+// C[t] = lin[t] - lin[t+K] (t^K = -1) over the 2K-1 planes of a linear
+// convolution, wrapping modulo 2^64
+__global__ __launch_bounds__(256) void k_negfold(const long long *__restrict__ lin,
+                                                 long long *__restrict__ C, size_t nn, int K)
+{
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)K * nn) return;
+    const int t = (int)(idx / nn);
+    const size_t e = idx % nn;
+    unsigned long long v = (unsigned long long)lin[idx];
+    if (t + K < 2 * K - 1) v -= (unsigned long long)lin[(size_t)(t + K) * nn + e];
+    C[idx] = (long long)v;
+}
+
 }  // namespace
+
+int mfh_launch_negfold(const int64_t *lin, int64_t *C, int n, int K, hipStream_t st)
+{
+    const size_t nn = (size_t)n * n, cnt = (size_t)K * nn;
+    hipLaunchKernelGGL(k_negfold, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, st,
+                       (const long long *)lin, (long long *)C, nn, K);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
 
 int mfh_launch_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign,
                         hipStream_t st)

@@ -605,6 +605,27 @@ int mfh_limbplane_mm(const uint16_t *A, const uint16_t *B, int n, int L, uint16_
     return limbplane_host(MFH_IN_U16, A, B, n, L, nullptr, out, RL);
 }
 
+int mfh_negconv(const int32_t *A, const int32_t *B, int K, int n, int64_t *C)
+{
+    if (!A || !B || !C || n < 1 || K < 1) return MFH_E_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t nn = (size_t)n * n;
+    TmpBufs t;
+    if (hipMalloc(&t.p[0], (size_t)K * nn * 4) != hipSuccess ||
+        hipMalloc(&t.p[1], (size_t)K * nn * 4) != hipSuccess ||
+        hipMalloc(&t.p[2], (size_t)(3 * K - 1) * nn * 8) != hipSuccess)
+        return MFH_E_NOMEM;
+    int64_t *lin = (int64_t *)t.p[2], *dC = lin + (size_t)(2 * K - 1) * nn;
+    MFH_HIP(hipMemcpy(t.p[0], A, (size_t)K * nn * 4, hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(t.p[1], B, (size_t)K * nn * 4, hipMemcpyHostToDevice));
+    if ((rc = mfh_launch_conv_limbplane(lin, t.p[0], t.p[1], 0, n, K, 0))) return rc;
+    if ((rc = mfh_launch_negfold(lin, dC, n, K, 0))) return rc;
+    MFH_HIP(hipDeviceSynchronize());
+    MFH_HIP(hipMemcpy(C, dC, (size_t)K * nn * 8, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+
 int mfh_fpx_encode(const float *X, int n, int L, int S, int32_t *X32)
 {
     return encode_host(X, 0, n, L, S, X32);

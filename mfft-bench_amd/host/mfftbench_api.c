@@ -153,14 +153,99 @@ void mfft_plan_describe(const mfft_plan *p, int n)
            mfft_plan_maxbits(p, n));
 }
 
+/* ---- recursive plan (src/mfft.c:474-527, 664-686) ------------------------
+ * The reference's planner for the recursive pointwise step: a negacyclic
+ * convolution of length 2^k over M_n(Z) with input magnitudes below 2^M
+ * either bottoms out in Karatsuba (3^k products, intermediates of about
+ * 2 + k + log2 n + 2M bits) or splits into 2^nu blocks (nu >= 2, 2 nu <=
+ * k + 1), each a length-2^(k+1-nu) problem with M + nu bits; a split is
+ * admissible while every intermediate stays within 62 bits.  The cheapest
+ * admissible choice wins (ties keep the earlier one).  The table is local
+ * to each call, so the planner is re-entrant. */
+typedef struct { long long cost; int nu, outbits, maxbits, ok; } negplan;
+#define NEG_K 26
+#define NEG_M 74
+typedef struct { negplan slot[NEG_K][NEG_M]; int done[NEG_K][NEG_M]; int ln; } negmemo;
+
+static int ilog2c(int x) { int r = 0; while ((1 << r) < x) r++; return r; }
+
+static negplan plan_neg(negmemo *m, int k, int M)
+{
+    negplan none = {0, 0, 0, 0, 0};
+    if (k < 0 || k >= NEG_K || M < 0 || M >= NEG_M) return none;
+    if (m->done[k][M]) return m->slot[k][M];
+    negplan best = none;
+    const int bbits = 2 + k + m->ln + 2 * M;
+    if (bbits <= 62) {
+        long long c = 1;
+        for (int i = 0; i < k; i++) c *= 3;
+        best = (negplan){c, 0, 1 + k + m->ln + 2 * M, bbits, 1};
+    }
+    for (int nu = 2; 2 * nu <= k + 1; nu++) {
+        negplan ch = plan_neg(m, k + 1 - nu, M + nu);
+        if (!ch.ok) continue;
+        int mx = ch.maxbits > nu + ch.outbits ? ch.maxbits : nu + ch.outbits;
+        if (mx > 62) continue;
+        long long c = ((long long)1 << nu) * ch.cost;
+        if (!best.ok || c < best.cost) best = (negplan){c, nu, ch.outbits + 1, mx, 1};
+    }
+    m->slot[k][M] = best;
+    m->done[k][M] = 1;
+    return best;
+}
+
+int mfft_plan_init_rec(mfft_plan *p, int L, int n, int sigma_override)
+{
+    if (L < 2 || (L & (L - 1)) || n < 1) return -1;
+    negmemo *m = calloc(1, sizeof *m);
+    if (!m) return -1;
+    m->ln = ilog2c(n);
+    int l = ilog2i(L), bs = 0;
+    long long best = -1;
+    for (int sigma = 1; sigma < l; sigma++) {
+        int S = 1 << sigma, NB = 2 * L / S, K = 2 * S;
+        if (2 * S * S < L || (2 * K) % NB || NB < 2) continue;
+        if (sigma_override > 0 && sigma != sigma_override) continue;
+        negplan pn = plan_neg(m, sigma + 1, LIMB_BITS + ilog2c(NB));
+        if (!pn.ok) continue;
+        long long c = (long long)NB * pn.cost;
+        if (best < 0 || c < best) { best = c; bs = sigma; }
+    }
+    free(m);
+    if (best < 0) return -1;
+    p->L = L; p->S = 1 << bs; p->NB = 2 * L / p->S; p->K = 2 * p->S;
+    p->g = 2 * p->K / p->NB;
+    p->rec = 1;
+    p->nprod = best;
+    return 0;
+}
+
+/* src/mfft.c:560-662: C = A * B in M_n(Z)[t]/(t^K + 1), K int32 planes in,
+ * K int64 planes out.  On the device: the linear convolution of the K
+ * planes (integer-ALU schoolbook, exact mod 2^64) folded by t^K = -1, the
+ * same result the reference's recursion and its Karatsuba base produce;
+ * Mbits only steers the reference's planner and is not needed here. */
+void ssa_negconv(int64_t *C, const int32_t *A, const int32_t *B, int K, int n, int Mbits,
+                 kernel_t kern)
+{
+    (void)Mbits;
+    t_last_error = 0;
+    if (kern != KERNEL_HIP) { fail("ssa_negconv", MFH_E_UNSUPPORTED); return; }
+    int rc = mfh_negconv(A, B, K, n, C);
+    if (rc) fail("ssa_negconv", rc);
+}
+
 /* ---- device context cache ------------------------------------------------ */
+/* A recursive plan (rec = 1) runs its outer transform as planned; its
+ * pointwise negacyclic products are the device's matrix-core products
+ * rather than a recursion, which gives the same exact result. */
 static int get_ctx(int n, int L, const mfft_plan *p, mfh_ctx **out)
 {
-    if (!p || p->rec) return MFH_E_ARG;
+    if (!p) return MFH_E_ARG;
     int key[4] = {n, L, p->S, p->NB};
     if (g_ctx && memcmp(key, g_key, sizeof key) == 0) { *out = g_ctx; return 0; }
     if (g_ctx) { mfh_destroy(g_ctx); g_ctx = NULL; }
-    mfh_plan hp = {p->L, p->S, p->NB, p->K, p->g, 0, p->nprod};
+    mfh_plan hp = {p->L, p->S, p->NB, p->K, p->g, 0, (long long)p->NB * p->K * p->K};
     int rc = mfh_create(&g_ctx, n, L, &hp);
     if (rc) { g_ctx = NULL; return rc; }
     memcpy(g_key, key, sizeof key);

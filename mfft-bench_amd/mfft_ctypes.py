@@ -94,6 +94,9 @@ def load(path=None):
         "mfh_set_timing": ([vp, i], i), "mfh_stage_times": ([vp, C.POINTER(C.c_float)], i),
         "mfh_work": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double)], i),
         "mfft_plan_init": ([pl, i, i], i), "mfft_plan_products": ([pl], C.c_longlong),
+        "mfft_plan_init_rec": ([pl, i, i, i], i),
+        "ssa_negconv": ([vp, vp, vp, i, i, i, i], None),
+        "mfh_negconv": ([vp, vp, i, i, vp], i),
         "mfft_plan_maxbits": ([pl, i], C.c_double),
         "mm_mfft": ([vp, vp, i, i, pl, i, vp, i], None),
         "mm_mfft_signed": ([vp, vp, i, i, pl, i, vp, i], None),
@@ -132,6 +135,13 @@ def check(rc, what=""):
 def plan(L, sigma=0):
     p = Plan()
     if load().mfft_plan_init(C.byref(p), L, sigma) != 0:
+        return None
+    return p
+
+
+def plan_rec(L, n, sigma=0):
+    p = Plan()
+    if load().mfft_plan_init_rec(C.byref(p), L, n, sigma) != 0:
         return None
     return p
 

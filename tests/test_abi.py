@@ -169,3 +169,37 @@ def test_schoolbook_rejects_cpu_leaves_and_leaves_outputs_untouched(lib):
     lib.mm_limbplane(A16.ctypes.data, A16.ctypes.data, n, L, M.KERNEL_PACKED, out.ctypes.data,
                      2 * L + 1)
     assert lib.mfft_last_error() == -7 and np.all(out == 7)
+
+
+# ---- recursive plan (src/mfft.c:474-527, 664-686) ---------------------------------
+def test_plan_rec_known_answers(lib):
+    """Product counts the reference publishes for mfft-rec (README.md:319-324,
+    measured at n = 32), and those of the workloads this library targets."""
+    import mfft_ctypes as M
+    for L, n, S, nprod in [(64, 32, 8, 1296), (512, 32, 16, 13824), (2048, 32, 32, 93312),
+                           (4096, 32, 64, 279936), (512, 256, 16, 15552),
+                           (128, 1024, 8, 2592), (32, 2048, 4, 432), (32, 4096, 4, 432)]:
+        p = M.plan_rec(L, n)
+        assert p is not None and p.rec == 1
+        assert (p.S, p.nprod) == (S, nprod), (L, n)
+        assert (p.NB, p.K, p.g) == (2 * L // S, 2 * S, 4 * S // (2 * L // S))
+        assert lib.mfft_plan_products(C.byref(p)) == nprod
+    assert M.plan_rec(2, 64) is None                   # no admissible block size
+    assert M.plan_rec(96, 64) is None                  # L not a power of two
+
+
+def test_plan_rec_matches_reference(lib, ref):
+    import mfft_ctypes as M
+    from oracle_ctypes import RefPlanStruct
+    ref.lib.mfft_plan_init_rec.argtypes = [C.POINTER(RefPlanStruct), C.c_int, C.c_int, C.c_int]
+    for L in [2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096]:
+        for n in [1, 3, 32, 64, 256, 1000, 1024, 4096, 1 << 16]:
+            for sigma in [0, 1, 2, 3, 5]:
+                rp = RefPlanStruct()
+                rrc = ref.lib.mfft_plan_init_rec(C.byref(rp), L, n, sigma)
+                p = M.Plan()
+                rc = lib.mfft_plan_init_rec(C.byref(p), L, n, sigma)
+                assert rc == rrc, (L, n, sigma)
+                if rc == 0:
+                    assert (p.L, p.S, p.NB, p.K, p.g, p.rec, p.nprod) == \
+                           (rp.L, rp.S, rp.NB, rp.K, rp.g, rp.rec, rp.nprod), (L, n, sigma)

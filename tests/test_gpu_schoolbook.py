@@ -1,8 +1,9 @@
 """GPU parity of the schoolbook entry points through the C-ABI: the leaf
-operator mm_accum (exact modulo 2^64 for any int32 entries), conv_limbplane
-and mm_limbplane, against Python integers, the oracle and the golden
-products; and the MFFT product checked against the schoolbook at the
-n=1024, 2048-bit workload on the device."""
+operator mm_accum (exact modulo 2^64 for any int32 entries), conv_limbplane,
+mm_limbplane and ssa_negconv, against Python integers, the oracle and the
+golden products; products under the recursive plan; and the MFFT product
+checked against the schoolbook at the n=1024, 2048-bit workload on the
+device."""
 import ctypes as C
 import json
 import os
@@ -118,3 +119,40 @@ def test_mfft_equals_schoolbook_n1024_w2048(gpu, orc, lib):
     A = orc.bigmat_rand(n, L, SEED)
     B = orc.bigmat_rand(n, L, SEED_B)
     assert orc.freivalds(A, B, n, L, o2, RL, nprimes=1)
+
+
+@pytest.mark.parametrize("K,n", [(4, 8), (8, 33), (16, 64), (32, 17)])
+def test_ssa_negconv(gpu, orc, lib, K, n):
+    """C = A B mod (t^K + 1): the linear limb convolution folded by t^K = -1
+    (src/mfft.c:529-557 is the reference's own base case)."""
+    rng = np.random.default_rng(K * n)
+    A = rng.integers(-2 ** 20, 2 ** 20, size=K * n * n).astype(np.int32)
+    B = rng.integers(-2 ** 20, 2 ** 20, size=K * n * n).astype(np.int32)
+    lin = orc.conv_limbplane(A, B, n, K).reshape(2 * K - 1, n * n)
+    want = lin[:K].copy()
+    want[:K - 1] -= lin[K:]
+    got = np.zeros(K * n * n, np.int64)
+    lib.ssa_negconv(got.ctypes.data, A.ctypes.data, B.ctypes.data, K, n, 36, gpu.KERNEL_HIP)
+    assert lib.mfft_last_error() == 0
+    assert np.array_equal(got.reshape(K, n * n), want)
+    # t^K = -1 on a basis element: t^(K-1) * t = -1
+    E1 = np.zeros(K * n * n, np.int32)
+    E2 = np.zeros(K * n * n, np.int32)
+    E1[(K - 1) * n * n:] = np.eye(n, dtype=np.int32).reshape(-1)
+    E2[n * n:2 * n * n] = np.eye(n, dtype=np.int32).reshape(-1)
+    lib.ssa_negconv(got.ctypes.data, E1.ctypes.data, E2.ctypes.data, K, n, 1, gpu.KERNEL_HIP)
+    ref = np.zeros((K, n * n), np.int64)
+    ref[0] = -np.eye(n, dtype=np.int64).reshape(-1)
+    assert np.array_equal(got.reshape(K, n * n), ref)
+
+
+@pytest.mark.parametrize("n,L", [(20, 8), (64, 64), (40, 128)])
+def test_mm_mfft_recursive_plan(gpu, orc, n, L):
+    """mm_mfft under mfft_plan_init_rec's plan gives the exact product."""
+    p = gpu.plan_rec(L, n)
+    assert p is not None and p.rec == 1
+    A = orc.bigmat_rand(n, L, SEED)
+    B = orc.bigmat_rand(n, L, SEED_B)
+    out, err = gpu.mm_mfft(A, B, n, L, p)
+    assert err == 0
+    assert np.array_equal(out, orc.mm_limbplane(A, B, n, L, 2 * L + 1))
