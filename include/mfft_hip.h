@@ -136,6 +136,11 @@ int mfh_limbplane_mm(const uint16_t *A, const uint16_t *B, int n, int L, uint16_
 int mfh_limbplane_mm_dev(mfh_ctx *ctx, const void *dA, const void *dB, int n, int L,
                          void *dCw, void *dOut, int RL);
 
+/* mm_bigint_ijk / mm_bigint_ikj (src/methods.c:22-86): entry-major uint16
+ * inputs (Aem[(i*n + k)*L + u]), plane-major RL-limb output; on the device
+ * the inputs are re-laid plane-major and multiplied by the schoolbook */
+int mfh_bigint_mm(const uint16_t *Aem, const uint16_t *Bem, int n, int L, uint16_t *out,
+                  int RL);
 /* negacyclic convolution C = A*B mod (t^K + 1) of K int32 planes into K
  * int64 planes (ssa_negconv, src/mfft.c:560-662): the limb-plane
  * convolution folded by t^K = -1 */

@@ -65,6 +65,13 @@ int  bigres_equal(const uint16_t *a, const uint16_t *b, int n, int RL,
 /* src/mfftbench.h:53-54: C += A*B if sign > 0, else C -= A*B */
 void mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign,
               kernel_t k);
+/* src/mfftbench.h:96-99: the textbook product on entry-major inputs
+ * (bigmat_to_entry_major), plane-major output; these have no kernel_t and
+ * always run on the device */
+void mm_bigint_ijk(const uint16_t *Aem, const uint16_t *Bem, int n, int L,
+                   uint16_t *out, int RL);
+void mm_bigint_ikj(const uint16_t *Aem, const uint16_t *Bem, int n, int L,
+                   uint16_t *out, int RL);
 /* src/mfftbench.h:100-101 */
 void mm_limbplane(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
                   kernel_t k, uint16_t *out, int RL);

@@ -134,6 +134,8 @@ int mfh_launch_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, i
                         hipStream_t st);
 int mfh_launch_conv_limbplane(int64_t *Cw, const void *A, const void *B, int u16, int n, int L,
                               hipStream_t st);
+// entry-major uint16 limbs (e[idx*L + u]) -> plane-major
+int mfh_launch_entry_to_plane(const uint16_t *e, uint16_t *p, int n, int L, hipStream_t st);
 // C[t] = lin[t] - lin[t+K], t < K (negacyclic fold of 2K-1 planes)
 int mfh_launch_negfold(const int64_t *lin, int64_t *C, int n, int K, hipStream_t st);
 int mfh_launch_copy16(void *dst, const void *src, size_t bytes, hipStream_t st);

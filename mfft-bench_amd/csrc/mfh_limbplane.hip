@@ -140,7 +140,40 @@ __global__ __launch_bounds__(256) void k_negfold(const long long *__restrict__ l
     C[idx] = (long long)v;
 }
 
+// entry-major limbs e[idx*L + u] -> plane-major p[u*nn + idx]
+// (src/bigmat.c:37-46 inverted), through a 64 x 64 LDS tile: rows of the
+// entry-major matrix are elements (blockIdx.x), columns limbs (blockIdx.y)
+__global__ __launch_bounds__(256) void k_entry_to_plane(const uint16_t *__restrict__ e,
+                                                        uint16_t *__restrict__ p, size_t nn,
+                                                        int L)
+{
+    __shared__ uint16_t tile[64][66];
+    const size_t r0 = (size_t)blockIdx.x * 64;
+    const int c0 = blockIdx.y * 64;
+    const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+    for (int r = ty; r < 64; r += 4) {
+        const size_t rr = r0 + r;
+        const int cc = c0 + tx;
+        if (rr < nn && cc < L) tile[r][tx] = e[rr * L + cc];
+    }
+    __syncthreads();
+    for (int c = ty; c < 64; c += 4) {
+        const int cc = c0 + c;
+        const size_t rr = r0 + tx;
+        if (rr < nn && cc < L) p[(size_t)cc * nn + rr] = tile[tx][c];
+    }
+}
+
 }  // namespace
+
+int mfh_launch_entry_to_plane(const uint16_t *e, uint16_t *p, int n, int L, hipStream_t st)
+{
+    const size_t nn = (size_t)n * n;
+    const dim3 grid((unsigned)((nn + 63) / 64), (unsigned)((L + 63) / 64));
+    hipLaunchKernelGGL(k_entry_to_plane, grid, dim3(256), 0, st, e, p, nn, L);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
 
 int mfh_launch_negfold(const int64_t *lin, int64_t *C, int n, int K, hipStream_t st)
 {

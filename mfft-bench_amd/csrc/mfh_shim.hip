@@ -605,6 +605,31 @@ int mfh_limbplane_mm(const uint16_t *A, const uint16_t *B, int n, int L, uint16_
     return limbplane_host(MFH_IN_U16, A, B, n, L, nullptr, out, RL);
 }
 
+int mfh_bigint_mm(const uint16_t *Aem, const uint16_t *Bem, int n, int L, uint16_t *out, int RL)
+{
+    if (!Aem || !Bem || !out || n < 1 || L < 1 || RL < 1) return MFH_E_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t nn = (size_t)n * n, in_b = (size_t)L * nn * 2;
+    const size_t cw_b = (size_t)(2 * L - 1) * nn * 8, out_b = (size_t)RL * nn * 2;
+    TmpBufs t;
+    if (hipMalloc(&t.p[0], 2 * in_b) != hipSuccess ||
+        hipMalloc(&t.p[1], 2 * in_b) != hipSuccess ||
+        hipMalloc(&t.p[2], cw_b + out_b) != hipSuccess)
+        return MFH_E_NOMEM;
+    uint16_t *eA = (uint16_t *)t.p[0], *eB = eA + (size_t)L * nn;
+    uint16_t *pA = (uint16_t *)t.p[1], *pB = pA + (size_t)L * nn;
+    void *dOut = (char *)t.p[2] + cw_b;
+    MFH_HIP(hipMemcpy(eA, Aem, in_b, hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(eB, Bem, in_b, hipMemcpyHostToDevice));
+    if ((rc = mfh_launch_entry_to_plane(eA, pA, n, L, 0))) return rc;
+    if ((rc = mfh_launch_entry_to_plane(eB, pB, n, L, 0))) return rc;
+    if ((rc = mfh_limbplane_mm_dev(nullptr, pA, pB, n, L, t.p[2], dOut, RL))) return rc;
+    MFH_HIP(hipDeviceSynchronize());
+    MFH_HIP(hipMemcpy(out, dOut, out_b, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+
 int mfh_negconv(const int32_t *A, const int32_t *B, int K, int n, int64_t *C)
 {
     if (!A || !B || !C || n < 1 || K < 1) return MFH_E_ARG;

@@ -312,6 +312,20 @@ void conv_limbplane(int64_t *Cw, const int32_t *A32, const int32_t *B32, int n, 
     if (rc) fail("conv_limbplane", rc);
 }
 
+void mm_bigint_ijk(const uint16_t *Aem, const uint16_t *Bem, int n, int L, uint16_t *out, int RL)
+{
+    t_last_error = 0;
+    int rc = mfh_bigint_mm(Aem, Bem, n, L, out, RL);
+    if (rc) fail("mm_bigint_ijk", rc);
+}
+
+void mm_bigint_ikj(const uint16_t *Aem, const uint16_t *Bem, int n, int L, uint16_t *out, int RL)
+{
+    t_last_error = 0;
+    int rc = mfh_bigint_mm(Aem, Bem, n, L, out, RL);
+    if (rc) fail("mm_bigint_ikj", rc);
+}
+
 void mm_limbplane(const uint16_t *Apl, const uint16_t *Bpl, int n, int L, kernel_t k,
                   uint16_t *out, int RL)
 {

@@ -97,6 +97,10 @@ def load(path=None):
         "mfft_plan_init_rec": ([pl, i, i, i], i),
         "ssa_negconv": ([vp, vp, vp, i, i, i, i], None),
         "mfh_negconv": ([vp, vp, i, i, vp], i),
+        "mfh_bigint_mm": ([vp, vp, i, i, vp, i], i),
+        "mm_bigint_ijk": ([vp, vp, i, i, vp, i], None),
+        "mm_bigint_ikj": ([vp, vp, i, i, vp, i], None),
+        "bigmat_to_entry_major": ([vp, i, i], C.c_void_p),
         "mfft_plan_maxbits": ([pl, i], C.c_double),
         "mm_mfft": ([vp, vp, i, i, pl, i, vp, i], None),
         "mm_mfft_signed": ([vp, vp, i, i, pl, i, vp, i], None),

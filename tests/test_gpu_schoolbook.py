@@ -156,3 +156,22 @@ def test_mm_mfft_recursive_plan(gpu, orc, n, L):
     out, err = gpu.mm_mfft(A, B, n, L, p)
     assert err == 0
     assert np.array_equal(out, orc.mm_limbplane(A, B, n, L, 2 * L + 1))
+
+
+@pytest.mark.parametrize("n,L", [(3, 4), (17, 16), (64, 64), (7, 130)])
+def test_mm_bigint_textbook_entry_major(gpu, orc, lib, n, L):
+    """mm_bigint_ijk / mm_bigint_ikj take entry-major inputs
+    (bigmat_to_entry_major, src/bigmat.c:37-46)."""
+    A = orc.bigmat_rand(n, L, SEED)
+    B = orc.bigmat_rand(n, L, SEED_B)
+    Aem = A.reshape(L, n * n).T.copy()
+    Bem = B.reshape(L, n * n).T.copy()
+    RL = 2 * L + 1
+    want = orc.mm_limbplane(A, B, n, L, RL)
+    for f in (lib.mm_bigint_ijk, lib.mm_bigint_ikj):
+        out = np.zeros(RL * n * n, np.uint16)
+        f(Aem.ctypes.data, Bem.ctypes.data, n, L, out.ctypes.data, RL)
+        assert lib.mfft_last_error() == 0
+        assert np.array_equal(out, want)
+    if n <= 17:
+        assert np.array_equal(want, orc.mm_bigint_ijk(A, B, n, L, RL))
