@@ -153,6 +153,82 @@ def cpu_baseline(n, L, nprod_total):
     }
 
 
+def method_table(args):
+    """The reference bench's result table (src/main.c:137-165) for the device
+    methods on one exact-track workload: the schoolbook (limbplane, the
+    speedup baseline as in src/main.c:293-297), the flat MFFT plan and the
+    recursive plan.  `products` is each method's n x n product count as the
+    reference defines it; `kernel_calls` is the reference's count of leaf
+    mm_accum calls, which the device methods do not make (0); `exact`
+    compares every limb with the schoolbook's result and checks it by
+    Freivalds' test."""
+    import numpy as np
+    import mfft_ctypes as M
+    n, W, ekind = CONFIGS[args.config]
+    if ekind == "fp32":
+        log("bench.py --table: exact-track workloads only (c1, c2, c3, c5)")
+        sys.exit(2)
+    signed = ekind == "signed"
+    L = W // 16
+    RL = 2 * L + 1
+    lib = M.load()
+    kind = M.MFH_IN_U16_SIGNED if signed else M.MFH_IN_U16
+    in_bytes = L * n * n * 2
+    dA, dB = M.DevBuf(in_bytes), M.DevBuf(in_bytes)
+    dRef, dO = M.DevBuf(RL * n * n * 2), M.DevBuf(RL * n * n * 2)
+    dCw = M.DevBuf((2 * L - 1) * n * n * 8)
+    M.check(lib.mfh_rand_u16_dev(None, dA.ptr, n, L, 12345))
+    M.check(lib.mfh_rand_u16_dev(None, dB.ptr, n, L, 12345 ^ 0xABCDEF))
+    M.check(lib.mfh_sync(None))
+
+    def timed(fn, steps):
+        fn()
+        M.check(lib.mfh_sync(None))
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        M.check(lib.mfh_sync(None))
+        return (time.perf_counter() - t0) / steps
+
+    rows = []
+    secs = timed(lambda: M.check(lib.mfh_limbplane_mm_dev(None, kind, dA.ptr, dB.ptr, n, L,
+                                                          dCw.ptr, dRef.ptr, RL)), 2)
+    ref_out = dRef.download(np.uint16, RL * n * n)
+    rows.append(["limbplane", "hip", L * L, 0, secs, ref_out])
+    for name, p in (("mfft", M.plan(L)), ("mfft-rec", M.plan_rec(L, n))):
+        if p is None:
+            continue
+        ctx = M.Ctx(n, L, p)
+        secs = timed(lambda: M.check(lib.mfh_mm_dev(ctx.h, kind, dA.ptr, dB.ptr, dO.ptr, RL)),
+                     max(1, args.steps))
+        ctx.sync()
+        out = dO.download(np.uint16, RL * n * n)
+        rows.append([name, "hip", p.nprod, 0, secs, out])
+        ctx.close()
+    A = host_rand_u16(n, L, 12345)
+    B = host_rand_u16(n, L, 12345 ^ 0xABCDEF)
+    base = rows[0][4]
+    for r in rows:
+        out = r[5]
+        ok = freivalds_check(A, B, out, n, L, RL, signed)
+        ok = ok and bool(np.array_equal(out, ref_out))
+        r[5] = ok
+    if args.csv:
+        print("method,kernel,products,kernel_calls,seconds,speedup,exact")
+        for name, k, prod, calls, secs, ok in rows:
+            print(f"{name},{k},{prod},{calls},{secs:.6f},{(base / secs if base else 0.0):.3f},"
+                  f"{'yes' if ok else 'NO'}")
+    else:
+        print(f"n={n} W={W} ({ekind}) on {lib.mfh_device_arch().decode()}")
+        print(f"\n{'method':<14} {'kernel':<9} {'n*n products':>12} {'seconds':>10} {'speedup':>9}  exact")
+        print("-" * 73)
+        for name, k, prod, calls, secs, ok in rows:
+            print(f"{name:<14} {k:<9} {prod:>12} {secs:>10.4f} {(base / secs if base else 0.0):>8.2f}x"
+                  f"  {'yes' if ok else 'NO!'}")
+    for b in (dA, dB, dRef, dO, dCw):
+        b.free()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +242,10 @@ def main():
                          "known-size kernel that HBM byte counters are calibrated against)")
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="HBM bytes per pointwise launch measured by rocprofv3 --pmc")
+    ap.add_argument("--table", action="store_true",
+                    help="instead of the JSON line: the reference bench's method table "
+                         "(src/main.c:137-165) for the device methods on this workload")
+    ap.add_argument("--csv", action="store_true", help="the same table as CSV")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -192,6 +272,10 @@ def main():
             f"{2 * nbytes / dt / 1e9:.1f} GB/s read+write")
         src.free()
         dst.free()
+        return
+
+    if args.table or args.csv:
+        method_table(args)
         return
 
     n, W, ekind = CONFIGS[args.config]

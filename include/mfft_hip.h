@@ -124,17 +124,20 @@ int mfh_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign
 int mfh_mm_accum_dev(mfh_ctx *ctx, void *dC, const void *dA, const void *dB, int n,
                      int sign);
 /* conv_limbplane (src/methods.c:94-104): Cw[w] = sum_{u+v=w} A_u B_v over
- * L limb planes (in_kind MFH_IN_I32: int32, MFH_IN_U16: uint16), 2L-1 int64
- * planes out */
+ * L limb planes (in_kind MFH_IN_I32: int32; MFH_IN_U16: uint16;
+ * MFH_IN_U16_SIGNED: uint16 with limb L-1 read as int16), 2L-1 int64 planes
+ * out */
 int mfh_limbplane_conv(const int32_t *A32, const int32_t *B32, int n, int L, int64_t *Cw);
 int mfh_limbplane_conv_dev(mfh_ctx *ctx, int in_kind, const void *dA, const void *dB,
                            int n, int L, void *dCw);
 /* mm_limbplane (src/methods.c:106-123): uint16 limb planes, the carry of
- * the convolution into RL uint16 limbs; dCw is 2L-1 int64 planes of scratch */
+ * the convolution into RL uint16 limbs; dCw is 2L-1 int64 planes of scratch;
+ * in_kind MFH_IN_U16 or MFH_IN_U16_SIGNED (two's complement entries, result
+ * mod 2^(16 RL) in two's complement) */
 int mfh_limbplane_mm(const uint16_t *A, const uint16_t *B, int n, int L, uint16_t *out,
                      int RL);
-int mfh_limbplane_mm_dev(mfh_ctx *ctx, const void *dA, const void *dB, int n, int L,
-                         void *dCw, void *dOut, int RL);
+int mfh_limbplane_mm_dev(mfh_ctx *ctx, int in_kind, const void *dA, const void *dB, int n,
+                         int L, void *dCw, void *dOut, int RL);
 
 /* mm_bigint_ijk / mm_bigint_ikj (src/methods.c:22-86): entry-major uint16
  * inputs (Aem[(i*n + k)*L + u]), plane-major RL-limb output; on the device

@@ -129,11 +129,11 @@ int mfh_launch_decode(mfh_ctx *c, const int64_t *Cw, int SAB, int fmt, void *out
                       int32_t *out2);
 int mfh_launch_rand_u16(void *dst, size_t count, uint64_t seed, hipStream_t st);
 // schoolbook (mfh_limbplane.hip): C += sign A B; Cw[w] = sum_{u+v=w} A_u B_v
-// over uint16 (u16 != 0) or int32 limb planes
+// over limb planes of kind MFH_IN_U16, MFH_IN_U16_SIGNED or MFH_IN_I32
 int mfh_launch_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign,
                         hipStream_t st);
-int mfh_launch_conv_limbplane(int64_t *Cw, const void *A, const void *B, int u16, int n, int L,
-                              hipStream_t st);
+int mfh_launch_conv_limbplane(int64_t *Cw, const void *A, const void *B, int in_kind, int n,
+                              int L, hipStream_t st);
 // entry-major uint16 limbs (e[idx*L + u]) -> plane-major
 int mfh_launch_entry_to_plane(const uint16_t *e, uint16_t *p, int n, int L, hipStream_t st);
 // C[t] = lin[t] - lin[t+K], t < K (negacyclic fold of 2K-1 planes)

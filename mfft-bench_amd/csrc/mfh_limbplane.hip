@@ -25,14 +25,21 @@ namespace {
 
 constexpr int TI = 64, TK = 32, PADW = TI + 4;
 
+// a limb; `sgn` reads a uint16 limb as int16 (the top limb of a two's
+// complement entry)
 template <class T>
-__device__ __forceinline__ int load_in(const T *p, size_t off) { return (int)p[off]; }
+__device__ __forceinline__ int load_in(const T *p, size_t off, bool sgn)
+{
+    if constexpr (sizeof(T) == 2) return sgn ? (int)(int16_t)p[off] : (int)p[off];
+    else return (int)p[off];
+}
 
 // one k slice of A (rows i0.., cols k0..) and of B (rows k0.., cols j0..)
 // into LDS; zero outside the n x n matrices
 template <class T>
 __device__ __forceinline__ void stage(int (*As)[PADW], int (*Bs)[PADW], const T *__restrict__ A,
-                                      const T *__restrict__ B, int n, int i0, int j0, int k0)
+                                      const T *__restrict__ B, int n, int i0, int j0, int k0,
+                                      bool sgnA = false, bool sgnB = false)
 {
     const int tid = threadIdx.x;
 #pragma unroll
@@ -41,11 +48,11 @@ __device__ __forceinline__ void stage(int (*As)[PADW], int (*Bs)[PADW], const T 
         // A: 32 consecutive k of one row per 32 threads (coalesced reads)
         const int ar = idx / TK, ak = idx % TK;
         const int gi = i0 + ar, gk = k0 + ak;
-        As[ak][ar] = (gi < n && gk < n) ? load_in(A, (size_t)gi * n + gk) : 0;
+        As[ak][ar] = (gi < n && gk < n) ? load_in(A, (size_t)gi * n + gk, sgnA) : 0;
         // B: 64 consecutive columns of one k row per 64 threads
         const int bk = idx / TI, bc = idx % TI;
         const int gkb = k0 + bk, gj = j0 + bc;
-        Bs[bk][bc] = (gkb < n && gj < n) ? load_in(B, (size_t)gkb * n + gj) : 0;
+        Bs[bk][bc] = (gkb < n && gj < n) ? load_in(B, (size_t)gkb * n + gj, sgnB) : 0;
     }
 }
 
@@ -93,11 +100,13 @@ __global__ __launch_bounds__(256) void k_mm_accum(long long *__restrict__ C,
         }
 }
 
-// Cw[w] for w = blockIdx.z: sum over the limb pairs (u, w-u) inside [0, L)
+// Cw[w] for w = blockIdx.z: sum over the limb pairs (u, w-u) inside [0, L);
+// signed_top reads limb L-1 of uint16 inputs as int16
 template <class T>
 __global__ __launch_bounds__(256) void k_conv_limbplane(long long *__restrict__ Cw,
                                                         const T *__restrict__ A,
-                                                        const T *__restrict__ B, int n, int L)
+                                                        const T *__restrict__ B, int n, int L,
+                                                        int signed_top)
 {
     __shared__ __align__(16) int As[TK][PADW];
     __shared__ __align__(16) int Bs[TK][PADW];
@@ -110,7 +119,8 @@ __global__ __launch_bounds__(256) void k_conv_limbplane(long long *__restrict__ 
     for (int u = ulo; u <= uhi; ++u) {
         const T *Au = A + (size_t)u * nn, *Bv = B + (size_t)(w - u) * nn;
         for (int k0 = 0; k0 < n; k0 += TK) {
-            stage(As, Bs, Au, Bv, n, i0, j0, k0);
+            stage(As, Bs, Au, Bv, n, i0, j0, k0, signed_top && u == L - 1,
+                  signed_top && w - u == L - 1);
             __syncthreads();
             mac_slice(acc, As, Bs, r0, c0);
             __syncthreads();
@@ -193,17 +203,20 @@ int mfh_launch_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, i
     return MFH_OK;
 }
 
-int mfh_launch_conv_limbplane(int64_t *Cw, const void *A, const void *B, int u16, int n, int L,
-                              hipStream_t st)
+int mfh_launch_conv_limbplane(int64_t *Cw, const void *A, const void *B, int in_kind, int n,
+                              int L, hipStream_t st)
 {
     const unsigned t = (unsigned)((n + TI - 1) / TI);
     const dim3 grid(t, t, (unsigned)(2 * L - 1));
-    if (u16)
+    if (in_kind == MFH_IN_U16 || in_kind == MFH_IN_U16_SIGNED)
         hipLaunchKernelGGL(k_conv_limbplane<uint16_t>, grid, dim3(256), 0, st, (long long *)Cw,
-                           (const uint16_t *)A, (const uint16_t *)B, n, L);
-    else
+                           (const uint16_t *)A, (const uint16_t *)B, n, L,
+                           (int)(in_kind == MFH_IN_U16_SIGNED));
+    else if (in_kind == MFH_IN_I32)
         hipLaunchKernelGGL(k_conv_limbplane<int32_t>, grid, dim3(256), 0, st, (long long *)Cw,
-                           (const int32_t *)A, (const int32_t *)B, n, L);
+                           (const int32_t *)A, (const int32_t *)B, n, L, 0);
+    else
+        return MFH_E_ARG;
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }

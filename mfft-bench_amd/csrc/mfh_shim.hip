@@ -548,16 +548,15 @@ int mfh_limbplane_conv_dev(mfh_ctx *c, int in_kind, const void *dA, const void *
                            int L, void *dCw)
 {
     if (!dA || !dB || !dCw || n < 1 || L < 1) return MFH_E_ARG;
-    if (in_kind != MFH_IN_U16 && in_kind != MFH_IN_I32) return MFH_E_ARG;
-    return mfh_launch_conv_limbplane((int64_t *)dCw, dA, dB, in_kind == MFH_IN_U16, n, L,
-                                     c ? c->stream : 0);
+    return mfh_launch_conv_limbplane((int64_t *)dCw, dA, dB, in_kind, n, L, c ? c->stream : 0);
 }
 
-int mfh_limbplane_mm_dev(mfh_ctx *c, const void *dA, const void *dB, int n, int L, void *dCw,
-                         void *dOut, int RL)
+int mfh_limbplane_mm_dev(mfh_ctx *c, int in_kind, const void *dA, const void *dB, int n, int L,
+                         void *dCw, void *dOut, int RL)
 {
     if (!dOut || RL < 1) return MFH_E_ARG;
-    int rc = mfh_limbplane_conv_dev(c, MFH_IN_U16, dA, dB, n, L, dCw);
+    if (in_kind != MFH_IN_U16 && in_kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
+    int rc = mfh_limbplane_conv_dev(c, in_kind, dA, dB, n, L, dCw);
     if (rc) return rc;
     return mfh_launch_carry_planes((const int64_t *)dCw, 2 * L - 1, (size_t)n * n,
                                    (uint16_t *)dOut, RL, c ? c->stream : 0);
@@ -583,7 +582,7 @@ int limbplane_host(int in_kind, const void *A, const void *B, int n, int L, int6
     if (out) dOut = (char *)t.p[2] + cw_b;
     MFH_HIP(hipMemcpy(t.p[0], A, (size_t)L * nn * eb, hipMemcpyHostToDevice));
     MFH_HIP(hipMemcpy(t.p[1], B, (size_t)L * nn * eb, hipMemcpyHostToDevice));
-    rc = out ? mfh_limbplane_mm_dev(nullptr, t.p[0], t.p[1], n, L, t.p[2], dOut, RL)
+    rc = out ? mfh_limbplane_mm_dev(nullptr, in_kind, t.p[0], t.p[1], n, L, t.p[2], dOut, RL)
              : mfh_limbplane_conv_dev(nullptr, in_kind, t.p[0], t.p[1], n, L, t.p[2]);
     if (rc) return rc;
     MFH_HIP(hipDeviceSynchronize());
@@ -624,7 +623,8 @@ int mfh_bigint_mm(const uint16_t *Aem, const uint16_t *Bem, int n, int L, uint16
     MFH_HIP(hipMemcpy(eB, Bem, in_b, hipMemcpyHostToDevice));
     if ((rc = mfh_launch_entry_to_plane(eA, pA, n, L, 0))) return rc;
     if ((rc = mfh_launch_entry_to_plane(eB, pB, n, L, 0))) return rc;
-    if ((rc = mfh_limbplane_mm_dev(nullptr, pA, pB, n, L, t.p[2], dOut, RL))) return rc;
+    if ((rc = mfh_limbplane_mm_dev(nullptr, MFH_IN_U16, pA, pB, n, L, t.p[2], dOut, RL)))
+        return rc;
     MFH_HIP(hipDeviceSynchronize());
     MFH_HIP(hipMemcpy(out, dOut, out_b, hipMemcpyDeviceToHost));
     return MFH_OK;
@@ -644,7 +644,7 @@ int mfh_negconv(const int32_t *A, const int32_t *B, int K, int n, int64_t *C)
     int64_t *lin = (int64_t *)t.p[2], *dC = lin + (size_t)(2 * K - 1) * nn;
     MFH_HIP(hipMemcpy(t.p[0], A, (size_t)K * nn * 4, hipMemcpyHostToDevice));
     MFH_HIP(hipMemcpy(t.p[1], B, (size_t)K * nn * 4, hipMemcpyHostToDevice));
-    if ((rc = mfh_launch_conv_limbplane(lin, t.p[0], t.p[1], 0, n, K, 0))) return rc;
+    if ((rc = mfh_launch_conv_limbplane(lin, t.p[0], t.p[1], MFH_IN_I32, n, K, 0))) return rc;
     if ((rc = mfh_launch_negfold(lin, dC, n, K, 0))) return rc;
     MFH_HIP(hipDeviceSynchronize());
     MFH_HIP(hipMemcpy(C, dC, (size_t)K * nn * 8, hipMemcpyDeviceToHost));

@@ -82,7 +82,7 @@ def load(path=None):
         "mfh_limbplane_conv": ([vp, vp, i, i, vp], i),
         "mfh_limbplane_conv_dev": ([vp, i, vp, vp, i, i, vp], i),
         "mfh_limbplane_mm": ([vp, vp, i, i, vp, i], i),
-        "mfh_limbplane_mm_dev": ([vp, vp, vp, i, i, vp, vp, i], i),
+        "mfh_limbplane_mm_dev": ([vp, i, vp, vp, i, i, vp, vp, i], i),
         "mm_accum": ([vp, vp, vp, i, i, i], None),
         "mm_limbplane": ([vp, vp, i, i, i, vp, i], None),
         "conv_limbplane": ([vp, vp, vp, i, i, i], None),

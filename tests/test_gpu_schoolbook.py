@@ -1,9 +1,8 @@
 """GPU parity of the schoolbook entry points through the C-ABI: the leaf
 operator mm_accum (exact modulo 2^64 for any int32 entries), conv_limbplane,
 mm_limbplane and ssa_negconv, against Python integers, the oracle and the
-golden products; products under the recursive plan; and the MFFT product
-checked against the schoolbook at the n=1024, 2048-bit workload on the
-device."""
+golden products; products under the recursive plan; and the MFFT products
+of the full-size workloads checked against the schoolbook on the device."""
 import ctypes as C
 import json
 import os
@@ -96,20 +95,24 @@ def test_mm_limbplane_matches_oracle(gpu, orc, lib, n, L):
     assert np.array_equal(out, orc.mm_limbplane(A, B, n, L, RL))
 
 
-def test_mfft_equals_schoolbook_n1024_w2048(gpu, orc, lib):
-    """The headline product computed twice on the device, by the MFFT path
+@pytest.mark.parametrize("n,W,signed", [(1024, 2048, False), (256, 8192, False),
+                                         (4096, 512, True)])
+def test_mfft_equals_schoolbook_full_size(gpu, orc, lib, n, W, signed):
+    """The full-size products computed twice on the device, by the MFFT path
     (int8 MFMA) and by the integer-ALU schoolbook, limb for limb."""
-    n, L = 1024, 128
+    L = W // 16
     RL = 2 * L + 1
-    print("[schoolbook] n=1024 W=2048", flush=True)
+    kind = gpu.MFH_IN_U16_SIGNED if signed else gpu.MFH_IN_U16
+    print(f"[schoolbook] n={n} W={W} signed={signed}", flush=True)
     with gpu.Ctx(n, L) as ctx:
         dA, dB = gpu.DevBuf(L * n * n * 2), gpu.DevBuf(L * n * n * 2)
         dO1, dO2 = gpu.DevBuf(RL * n * n * 2), gpu.DevBuf(RL * n * n * 2)
         dCw = gpu.DevBuf((2 * L - 1) * n * n * 8)
         gpu.check(lib.mfh_rand_u16_dev(ctx.h, dA.ptr, n, L, SEED))
         gpu.check(lib.mfh_rand_u16_dev(ctx.h, dB.ptr, n, L, SEED_B))
-        gpu.check(lib.mfh_mm_dev(ctx.h, gpu.MFH_IN_U16, dA.ptr, dB.ptr, dO1.ptr, RL))
-        gpu.check(lib.mfh_limbplane_mm_dev(ctx.h, dA.ptr, dB.ptr, n, L, dCw.ptr, dO2.ptr, RL))
+        gpu.check(lib.mfh_mm_dev(ctx.h, kind, dA.ptr, dB.ptr, dO1.ptr, RL))
+        gpu.check(lib.mfh_limbplane_mm_dev(ctx.h, kind, dA.ptr, dB.ptr, n, L, dCw.ptr,
+                                            dO2.ptr, RL))
         ctx.sync()
         o1 = dO1.download(np.uint16, RL * n * n)
         o2 = dO2.download(np.uint16, RL * n * n)
@@ -118,7 +121,7 @@ def test_mfft_equals_schoolbook_n1024_w2048(gpu, orc, lib):
     assert np.array_equal(o1, o2)
     A = orc.bigmat_rand(n, L, SEED)
     B = orc.bigmat_rand(n, L, SEED_B)
-    assert orc.freivalds(A, B, n, L, o2, RL, nprimes=1)
+    assert orc.freivalds(A, B, n, L, o2, RL, signed_top=signed, nprimes=1)
 
 
 @pytest.mark.parametrize("K,n", [(4, 8), (8, 33), (16, 64), (32, 17)])
@@ -175,3 +178,28 @@ def test_mm_bigint_textbook_entry_major(gpu, orc, lib, n, L):
         assert np.array_equal(out, want)
     if n <= 17:
         assert np.array_equal(want, orc.mm_bigint_ijk(A, B, n, L, RL))
+
+
+@pytest.mark.parametrize("n,L", [(9, 4), (40, 32)])
+def test_limbplane_signed_top_limb(gpu, orc, lib, n, L):
+    """Two's complement entries (limb L-1 read as int16) through the device
+    schoolbook equal the MFFT path's signed product and the oracle's exact
+    entries."""
+    A = orc.bigmat_rand(n, L, SEED + 3)
+    B = orc.bigmat_rand(n, L, SEED_B + 3)
+    RL = 2 * L + 1
+    dA, dB = gpu.DevBuf(A.nbytes), gpu.DevBuf(B.nbytes)
+    dA.upload(A)
+    dB.upload(B)
+    dCw, dO = gpu.DevBuf((2 * L - 1) * n * n * 8), gpu.DevBuf(RL * n * n * 2)
+    gpu.check(lib.mfh_limbplane_mm_dev(None, gpu.MFH_IN_U16_SIGNED, dA.ptr, dB.ptr, n, L,
+                                       dCw.ptr, dO.ptr, RL))
+    gpu.check(lib.mfh_sync(None))
+    got = dO.download(np.uint16, RL * n * n)
+    for b in (dA, dB, dCw, dO):
+        b.free()
+    want, err = gpu.mm_mfft(A, B, n, L, gpu.plan(L), signed=True)
+    assert err == 0 and np.array_equal(got, want)
+    for i, j in [(0, 0), (n - 1, 2), (3, n - 1)]:
+        assert np.array_equal(got.reshape(RL, n * n)[:, i * n + j],
+                              orc.entry_exact(A, B, n, L, i, j, RL, signed_top=True))
