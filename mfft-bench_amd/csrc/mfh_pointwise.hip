@@ -55,11 +55,17 @@ constexpr int pmod(int a, int m) { return ((a % m) + m) % m; }
 // DMA: fill the round buffer with buffer-to-LDS copies after each round
 // (no staging registers; the fill latency is hidden by the other
 // workgroups on the CU) instead of from registers loaded a round ahead.
-template <int K_, int T_, int WBI_, int WBJ_, int KB_ = 1, int WPE_ = 2, bool DMA_ = false>
+// BREG: (copy fills only) a wave reads all its B fragments of the round into
+// registers up front, like the A fragments, so both tiles of the next round
+// are copied in while this round's MFMAs run from registers.
+template <int K_, int T_, int WBI_, int WBJ_, int KB_ = 1, int WPE_ = 2, bool DMA_ = false,
+          int BREG_ = 0>
 struct PwCfg {
     static constexpr int K = K_, T = T_, WBI = WBI_, WBJ = WBJ_, KB = KB_, WPE = WPE_;
     static constexpr bool DMA = DMA_;
+    static constexpr int BREG = BREG_;   // 1: B fragments in registers
     static_assert(!DMA || (KB == 1 && T == K), "copy fills: one k block, whole-ring waves");
+    static_assert(!BREG || DMA, "B fragments in registers: copy fills only");
     static_assert(KB == 1 || KB == 2, "one or two k blocks per fill");
     static constexpr int G = K / T;                 // t-groups per block
     static constexpr int WAVES = WBI * WBJ * G;
@@ -97,6 +103,29 @@ __device__ __forceinline__ void pw_round(v4i (&acc)[Cfg::T], const v4i *__restri
         v4i af[K];
 #pragma unroll
         for (int c1 = 0; c1 < K; ++c1) af[c1] = la[c1 * SA];
+        if constexpr (Cfg::BREG) {
+            v4i bf[K];
+#pragma unroll
+            for (int c2 = 0; c2 < K; ++c2) bf[c2] = lb[c2 * SB];
+            after_a();
+#pragma unroll
+            for (int st = 0; st < K; ++st) {
+                const int c2 = ASC ? st : K - 1 - st;
+                if (ASC && c2 >= 1) acc[c2 - 1] = -acc[c2 - 1];
+                if (!ASC) acc[c2] = -acc[c2];
+                const int lead = ASC ? c2 : (c2 + K - 1) % K;
+#pragma unroll
+                for (int o = 0; o < T; ++o) {
+                    const int t = (lead + o) % K;
+                    acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[pmod(t - c2, K)], bf[c2],
+                                                                   acc[t], 0, 0, 0);
+                }
+                issue(st);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (ASC) acc[K - 1] = -acc[K - 1];
+            return;
+        }
         after_a();
         v4i bq[3];
         bq[0] = lb[(ASC ? 0 : K - 1) * SB];
@@ -422,12 +451,23 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
             // is copied in while this round's MFMAs run; the B tile follows
             // after the round.  The last barrier waits for both copies.
             const bool more = nxt.m < NCLASS;
-            pw_round<Cfg, ASC, 0>(acc, la, lb, NoIssue{}, [&]() {
+            if constexpr (Cfg::BREG == 1) {
+                // every wave holds its A and B fragments: copy both tiles
+                pw_round<Cfg, ASC, 0>(acc, la, lb, NoIssue{}, [&]() {
+                    lds_barrier();
+                    if (more) {
+                        dma_a(nxt);
+                        dma_b(nxt);
+                    }
+                });
+            } else {
+                pw_round<Cfg, ASC, 0>(acc, la, lb, NoIssue{}, [&]() {
+                    lds_barrier();
+                    if (more) dma_a(nxt);
+                });
                 lds_barrier();
-                if (more) dma_a(nxt);
-            });
-            lds_barrier();
-            if (more) dma_b(nxt);
+                if (more) dma_b(nxt);
+            }
             round_barrier();
             cur = nxt;
             if (cur.m < NCLASS) nxt = next_of(cur);
@@ -523,13 +563,13 @@ int mfh_launch_pointwise(mfh_ctx *c)
 {
     switch (c->K) {
     case 4:  return launch_cfg<PwCfg<4, 4, 2, 2>>(c);
-    // K = 8: 8 or 16 waves per workgroup at 4 waves per SIMD (122 / 114
-    // VGPRs); 64 x 32 tiles, or 64 x 64 from n = 4096 on (measured best)
-    case 8:
-        return c->np >= 4096 ? launch_cfg<PwCfg<8, 8, 4, 4, 1, 4>>(c)
-                             : launch_cfg<PwCfg<8, 8, 4, 2, 1, 4>>(c);
-    // K = 16: copy fills (no staging registers), two workgroups per CU
-    case 16: return launch_cfg<PwCfg<16, 16, 2, 2, 1, 2, true>>(c);
+    // K = 8 and K = 16: copy fills with the B fragments held in registers,
+    // one workgroup per CU (64 x 64 tiles, 16 waves at 4 per SIMD, 116
+    // VGPRs; 64 x 32 tiles, 8 waves at 2 per SIMD, 214 VGPRs): measured
+    // 11-13 % (K = 8) and 5 % (K = 16) faster than two workgroups per CU
+    // with half the tile
+    case 8:  return launch_cfg<PwCfg<8, 8, 4, 4, 1, 4, true, 1>>(c);
+    case 16: return launch_cfg<PwCfg<16, 16, 4, 2, 1, 2, true, 1>>(c);
     case 32: return launch_cfg<PwCfg<32, 8, 1, 1>>(c);
     default: return MFH_E_UNSUPPORTED;
     }
