@@ -57,13 +57,15 @@ constexpr int pmod(int a, int m) { return ((a % m) + m) % m; }
 // workgroups on the CU) instead of from registers loaded a round ahead.
 // BREG: (copy fills only) a wave reads all its B fragments of the round into
 // registers up front, like the A fragments, so both tiles of the next round
-// are copied in while this round's MFMAs run from registers.
+// are copied in while this round's MFMAs run from registers.  BREG = 1: the
+// barrier that frees the buffer and the copies come before the first MFMA;
+// BREG = s + 2: after step s of the round's MFMAs.
 template <int K_, int T_, int WBI_, int WBJ_, int KB_ = 1, int WPE_ = 2, bool DMA_ = false,
           int BREG_ = 0>
 struct PwCfg {
     static constexpr int K = K_, T = T_, WBI = WBI_, WBJ = WBJ_, KB = KB_, WPE = WPE_;
     static constexpr bool DMA = DMA_;
-    static constexpr int BREG = BREG_;   // 1: B fragments in registers
+    static constexpr int BREG = BREG_;
     static_assert(!DMA || (KB == 1 && T == K), "copy fills: one k block, whole-ring waves");
     static_assert(!BREG || DMA, "B fragments in registers: copy fills only");
     static_assert(KB == 1 || KB == 2, "one or two k blocks per fill");
@@ -289,6 +291,7 @@ struct NoIssue {
 // its digit pairs (r, m-r) and, for each, the np/64 k blocks.
 struct RoundPos {
     int m, idx;            // class and round index inside the class
+    int r, kb;             // its digit pair's A plane r and k block (idx = (r - rlo) * kblocks + kb)
 };
 // B8: class m holds the digit pairs (r, m-r); K7: class p is the single
 // Karatsuba product of plane p with plane p.
@@ -370,12 +373,9 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     v4i R[Cfg::DMA ? 1 : KB * NF];
     // copy fills (DMA mode): the round's A or B tiles straight into LDS
     auto srcs = [&](RoundPos q, const int8_t *&a0, const int8_t *&b0) {
-        int rlo, np2;
-        class_pairs<MODE>(q.m, rlo, np2);
-        const int r = rlo + q.idx / kblocks, kb = q.idx % kblocks;
-        const int s = MODE == MFH_MODE_K7 ? r : q.m - r;
-        a0 = a_blk + (size_t)r * plane + kb * MFH_KBLK;
-        b0 = b_blk + (size_t)s * plane + kb * MFH_KBLK;
+        const int s = MODE == MFH_MODE_K7 ? q.r : q.m - q.r;
+        a0 = a_blk + (size_t)q.r * plane + q.kb * MFH_KBLK;
+        b0 = b_blk + (size_t)s * plane + q.kb * MFH_KBLK;
     };
     auto dma_a = [&](RoundPos q) {
         const int8_t *a0, *b0;
@@ -395,9 +395,7 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     };
     auto gload = [&](RoundPos q) {
         if constexpr (Cfg::DMA) return;
-        int rlo, np2;
-        class_pairs<MODE>(q.m, rlo, np2);
-        const int r = rlo + q.idx / kblocks, kb = q.idx % kblocks;
+        const int r = q.r, kb = q.kb;
         const int s = MODE == MFH_MODE_K7 ? r : q.m - r;
 #pragma unroll
         for (int sb = 0; sb < KB; ++sb) {
@@ -422,12 +420,15 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     auto next_of = [&](RoundPos q) {
         int rlo, np2;
         class_pairs<MODE>(q.m, rlo, np2);
-        if (q.idx + 1 < np2 * kblocks) return RoundPos{q.m, q.idx + 1};
-        return RoundPos{q.m + 1, 0};
+        if (q.kb + 1 < kblocks) return RoundPos{q.m, q.idx + 1, q.r, q.kb + 1};
+        if (q.idx + 1 < np2 * kblocks) return RoundPos{q.m, q.idx + 1, q.r + 1, 0};
+        int rlo2, np3;
+        class_pairs<MODE>(q.m + 1, rlo2, np3);
+        return RoundPos{q.m + 1, 0, rlo2, 0};
     };
 
     // prologue: round (0,0) into LDS, round after it into registers
-    RoundPos cur{0, 0};
+    RoundPos cur{0, 0, 0, 0};
     RoundPos nxt = next_of(cur);
     if constexpr (Cfg::DMA) {
         dma_a(cur);
@@ -458,6 +459,17 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
                     if (more) {
                         dma_a(nxt);
                         dma_b(nxt);
+                    }
+                });
+            } else if constexpr (Cfg::BREG >= 2) {
+                // the same after step BREG-2 of the round's MFMAs
+                pw_round<Cfg, ASC, 0>(acc, la, lb, [&](int st) {
+                    if (st == Cfg::BREG - 2) {
+                        lds_barrier();
+                        if (more) {
+                            dma_a(nxt);
+                            dma_b(nxt);
+                        }
                     }
                 });
             } else {
@@ -567,9 +579,11 @@ int mfh_launch_pointwise(mfh_ctx *c)
     // one workgroup per CU (64 x 64 tiles, 16 waves at 4 per SIMD, 116
     // VGPRs; 64 x 32 tiles, 8 waves at 2 per SIMD, 214 VGPRs): measured
     // 11-13 % (K = 8) and 5 % (K = 16) faster than two workgroups per CU
-    // with half the tile
+    // with half the tile.  For K = 16 the barrier and the copies come after
+    // the round's third step of MFMAs, so the MFMAs start as soon as this
+    // wave's fragments are in (another 4 %; for K = 8 it is slower).
     case 8:  return launch_cfg<PwCfg<8, 8, 4, 4, 1, 4, true, 1>>(c);
-    case 16: return launch_cfg<PwCfg<16, 16, 4, 2, 1, 2, true, 1>>(c);
+    case 16: return launch_cfg<PwCfg<16, 16, 4, 2, 1, 2, true, 4>>(c);
     case 32: return launch_cfg<PwCfg<32, 8, 1, 1>>(c);
     default: return MFH_E_UNSUPPORTED;
     }
