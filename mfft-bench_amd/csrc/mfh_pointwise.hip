@@ -309,16 +309,19 @@ __device__ __forceinline__ void class_pairs(int m, int &rlo, int &npairs)
 }
 
 // One workgroup: a (16*WBI) x (16*WBJ) block of elements at one evaluation
-// point, all K ring coefficients, all five digit-weight classes in turn.
-// Each class's int32 result is stored as soon as the class is complete, so
-// the only long-lived state is one int32 accumulator per (t, element); the
-// kernel fits two workgroups per CU.  Without Cfg::DMA rounds are
-// double-buffered through registers: while a round's MFMAs read the LDS
-// buffer, the next round's fragments stream from global memory into VGPRs;
-// after the round they are written to LDS (one buffer per workgroup).  With
-// Cfg::DMA the buffer is refilled by buffer-to-LDS copies: the A tile while
-// the round runs (once every wave holds its A fragments), the B tile after
-// it, while the other workgroups on the CU keep the MFMA units busy.
+// point, all K ring coefficients, all digit-weight classes in turn.  Each
+// class's int32 result is stored as soon as the class is complete, so the
+// only long-lived state is one int32 accumulator per (t, element).  Without
+// Cfg::DMA rounds are double-buffered through registers: while a round's
+// MFMAs read the LDS buffer, the next round's fragments stream from global
+// memory into VGPRs; after the round they are written to LDS (one buffer
+// per workgroup).  With Cfg::DMA the buffer is refilled by buffer-to-LDS
+// copies: with Cfg::BREG every wave first reads all its A and B fragments of
+// the round into registers, and once every wave has (a barrier, before the
+// first MFMA or after an early step) both tiles of the next round are
+// copied in while the MFMAs run; without it the A tile is copied during the
+// round and the B tile after it, while the other workgroups on the CU keep
+// the MFMA units busy.
 //
 // Output: class m of (j, i, j', t) at mfh_c5_index + m * mfh_c5_class_stride.
 // Accumulator bound: a class has at most 3 digit pairs x np/64 rounds of at
