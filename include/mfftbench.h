@@ -59,6 +59,28 @@ void normalize_planes(const int64_t *acc, int nplanes, int n,
 int  bigres_equal(const uint16_t *a, const uint16_t *b, int n, int RL,
                   int *bad_i, int *bad_j, int *bad_w);           /* :62-75 */
 
+/* ---- instrumentation the reference bench reads (src/mfftbench.h:56-71) --
+ * g_kernel_calls counts mm_accum calls (the device MFFT path makes none).
+ * With g_mfft_profile set, mm_mfft / conv_mfft add their device stage
+ * times (HIP events) to g_mfft_prof: transform = forward transforms +
+ * inverse (which also folds, and on the exact track carries), pointwise =
+ * the batched MFMA step; packing and op lists are fused into the forward
+ * kernel (pack = build_ops = 0), fold into the inverse (fold = 0). */
+extern long long g_kernel_calls;
+typedef struct {
+    double pack;
+    double build_ops;
+    double transform;
+    double pointwise;
+    double fold;
+    long long n_build;
+    long long n_fft;
+} mfft_profile_t;
+extern int g_mfft_profile;
+extern mfft_profile_t g_mfft_prof;
+void mfft_profile_reset(void);
+void mfft_profile_print(const char *label);
+
 /* ---- the leaf operator and the limb-plane schoolbook ---------------------
  * k must be KERNEL_HIP: integer-ALU kernels on the device, exact modulo 2^64
  * for any int32 entries like the reference's int64 leaves. */

@@ -23,6 +23,41 @@ static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
 static mfh_ctx *g_ctx;
 static int g_key[4];
 
+long long g_kernel_calls;
+int g_mfft_profile;
+mfft_profile_t g_mfft_prof;
+
+void mfft_profile_reset(void) { memset(&g_mfft_prof, 0, sizeof g_mfft_prof); }
+
+/* src/mfft.c:51-73: the same report */
+void mfft_profile_print(const char *label)
+{
+    const mfft_profile_t *p = &g_mfft_prof;
+    double tot = p->pack + p->build_ops + p->transform + p->pointwise + p->fold;
+    if (tot <= 0) tot = 1e-30;
+    printf("profile %s:\n"
+           "  pack        %8.4f s  (%5.1f%%)\n"
+           "  build_ops   %8.4f s  (%5.1f%%)  calls %lld\n"
+           "  transform   %8.4f s  (%5.1f%%)  fft runs %lld\n"
+           "  pointwise   %8.4f s  (%5.1f%%)\n"
+           "  fold        %8.4f s  (%5.1f%%)\n"
+           "  total       %8.4f s\n",
+           label ? label : "mfft", p->pack, 100.0 * p->pack / tot, p->build_ops,
+           100.0 * p->build_ops / tot, p->n_build, p->transform, 100.0 * p->transform / tot,
+           p->n_fft, p->pointwise, 100.0 * p->pointwise / tot, p->fold,
+           100.0 * p->fold / tot, tot);
+}
+
+/* stage times of the product just run on `c` into g_mfft_prof */
+static void profile_add(mfh_ctx *c)
+{
+    float ms[5];
+    if (mfh_stage_times(c, ms) != MFH_OK) return;
+    g_mfft_prof.transform += (ms[0] + ms[2] + ms[3]) * 1e-3;
+    g_mfft_prof.pointwise += ms[1] * 1e-3;
+    g_mfft_prof.n_fft += 3;
+}
+
 int mfft_last_error(void) { return t_last_error; }
 const char *mfft_strerror(int code) { return mfh_strerror(code); }
 
@@ -263,7 +298,11 @@ static void mm_common(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
     pthread_mutex_lock(&g_lock);
     mfh_ctx *c = NULL;
     int rc = get_ctx(n, L, p, &c);
-    if (!rc) rc = mfh_mm(c, kind, Apl, Bpl, out, RL);
+    if (!rc) {
+        mfh_set_timing(c, g_mfft_profile != 0);
+        rc = mfh_mm(c, kind, Apl, Bpl, out, RL);
+        if (!rc && g_mfft_profile) profile_add(c);
+    }
     pthread_mutex_unlock(&g_lock);
     if (rc) fail(name, rc);
 }
@@ -289,7 +328,11 @@ void conv_mfft(int64_t *Cw, const int32_t *A32, const int32_t *B32,
     pthread_mutex_lock(&g_lock);
     mfh_ctx *c = NULL;
     int rc = get_ctx(n, L, p, &c);
-    if (!rc) rc = mfh_conv(c, A32, B32, Cw);
+    if (!rc) {
+        mfh_set_timing(c, g_mfft_profile != 0);
+        rc = mfh_conv(c, A32, B32, Cw);
+        if (!rc && g_mfft_profile) profile_add(c);
+    }
     pthread_mutex_unlock(&g_lock);
     if (rc) fail("conv_mfft", rc);
 }
@@ -297,6 +340,7 @@ void conv_mfft(int64_t *Cw, const int32_t *A32, const int32_t *B32,
 /* ---- schoolbook (src/kernel.c:1015-1033, src/methods.c:94-123) ---------- */
 void mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, int sign, kernel_t k)
 {
+    g_kernel_calls++;              /* src/kernel.c:1018 */
     t_last_error = 0;
     if (k != KERNEL_HIP) { fail("mm_accum", MFH_E_UNSUPPORTED); return; }
     int rc = mfh_mm_accum(C, A, B, n, sign);

@@ -33,6 +33,13 @@ class Plan(C.Structure):
         return f"Plan(L={self.L}, S={self.S}, NB={self.NB}, K={self.K}, g={self.g})"
 
 
+class ProfileT(C.Structure):
+    """mfft_profile_t (src/mfftbench.h:59-67)"""
+    _fields_ = [("pack", C.c_double), ("build_ops", C.c_double), ("transform", C.c_double),
+                ("pointwise", C.c_double), ("fold", C.c_double), ("n_build", C.c_longlong),
+                ("n_fft", C.c_longlong)]
+
+
 class FpxCtx(C.Structure):
     _fields_ = [("n", C.c_int), ("L", C.c_int), ("sig", C.c_int),
                 ("SA", C.c_int), ("SB", C.c_int),
@@ -118,6 +125,7 @@ def load(path=None):
         "fpx_decode_f64": ([C.POINTER(FpxCtx), vp], None),
         "fpx_decode_ld": ([C.POINTER(FpxCtx), vp], None),
         "fpx_mm_f64": ([C.POINTER(FpxCtx), pl, vp], i),
+        "mfft_profile_reset": ([], None), "mfft_profile_print": ([C.c_char_p], None),
         "mfft_last_error": ([], i), "mfft_strerror": ([i], C.c_char_p),
         "kernel_name": ([i], C.c_char_p), "kernel_from_name": ([C.c_char_p], i),
         "now_sec": ([], C.c_double),

@@ -203,3 +203,23 @@ def test_plan_rec_matches_reference(lib, ref):
                 if rc == 0:
                     assert (p.L, p.S, p.NB, p.K, p.g, p.rec, p.nprod) == \
                            (rp.L, rp.S, rp.NB, rp.K, rp.g, rp.rec, rp.nprod), (L, n, sigma)
+
+
+def test_profile_globals_and_leaf_call_counter(lib):
+    """g_kernel_calls / g_mfft_profile / g_mfft_prof (src/mfftbench.h:56-71)
+    are exported with the reference's layout; mm_accum counts its calls."""
+    import mfft_ctypes as M
+    calls = C.c_longlong.in_dll(lib, "g_kernel_calls")
+    prof = M.ProfileT.in_dll(lib, "g_mfft_prof")
+    flag = C.c_int.in_dll(lib, "g_mfft_profile")
+    assert flag.value == 0
+    before = calls.value
+    n = 2
+    A = np.ones(n * n, np.int32)
+    Cm = np.zeros(n * n, np.int64)
+    lib.mm_accum(Cm.ctypes.data, A.ctypes.data, A.ctypes.data, n, 1, M.KERNEL_PACKED)
+    assert calls.value == before + 1
+    prof.pointwise = 1.0
+    lib.mfft_profile_reset()
+    assert (prof.pack, prof.transform, prof.pointwise, prof.n_fft) == (0.0, 0.0, 0.0, 0)
+    assert C.sizeof(M.ProfileT) == 56

@@ -203,3 +203,24 @@ def test_limbplane_signed_top_limb(gpu, orc, lib, n, L):
     for i, j in [(0, 0), (n - 1, 2), (3, n - 1)]:
         assert np.array_equal(got.reshape(RL, n * n)[:, i * n + j],
                               orc.entry_exact(A, B, n, L, i, j, RL, signed_top=True))
+
+
+def test_profile_records_device_stages(gpu, orc, lib):
+    """With g_mfft_profile set, mm_mfft adds its device stage times to
+    g_mfft_prof the way the reference bench reads them (src/main.c:370)."""
+    n, L = 64, 64
+    flag = C.c_int.in_dll(lib, "g_mfft_profile")
+    prof = gpu.ProfileT.in_dll(lib, "g_mfft_prof")
+    lib.mfft_profile_reset()
+    flag.value = 1
+    try:
+        A = orc.bigmat_rand(n, L, SEED)
+        B = orc.bigmat_rand(n, L, SEED_B)
+        out, err = gpu.mm_mfft(A, B, n, L, gpu.plan(L))
+        out2, err2 = gpu.mm_mfft(A, B, n, L, gpu.plan(L))
+    finally:
+        flag.value = 0
+    assert err == 0 and err2 == 0 and np.array_equal(out, out2)
+    assert prof.n_fft == 6 and prof.transform > 0 and prof.pointwise > 0
+    assert prof.pack == 0 and prof.build_ops == 0 and prof.fold == 0
+    lib.mfft_profile_print(b"mfft-hip")
