@@ -116,7 +116,7 @@ def test_carry_runs_of_ones_and_zeros(gpu):
     chains cross every carry-lookahead run boundary, in both directions.
     (-1)(1) summed over n is -n; (-1)(-1) is +n; (2^W - 1)(1) unsigned is
     n (2^W - 1).  Closed forms, so no oracle is needed."""
-    for n, L in [(64, 128), (16, 64), (32, 32)]:
+    for n, L in [(64, 128), (16, 64), (32, 32), (16, 512)]:
         RL = 2 * L + 1
         ones = np.full(L * n * n, 0xFFFF, np.uint16)             # -1 signed, 2^W-1 unsigned
         one = np.zeros(L * n * n, np.uint16)
