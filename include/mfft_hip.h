@@ -59,7 +59,12 @@ const char *mfh_device_arch(void);
 
 /* Workspace for products of n x n matrices with L limbs under `plan`.
  * Rejects plans whose worst case breaks the stated accumulator bounds
- * (int8 digits, int32 MFMA accumulators, int64 transform values). */
+ * (int8 digits, int32 MFMA accumulators, int64 transform values).  The
+ * int32 bound depends on the digit mode: sizes that only the 6-product mode
+ * admits (n up to about 8128 at K = 16, against 2688 for the 9-product
+ * mode) serve the exact-track products, while conv and fixed-point-float
+ * products, which take the 9-product mode where plain 6-product digits do
+ * not fit, return MFH_E_BOUND. */
 int  mfh_create(mfh_ctx **ctx, int n, int L, const mfh_plan *plan);
 void mfh_destroy(mfh_ctx *ctx);
 /* device bytes held by the context */

@@ -73,11 +73,12 @@ __host__ __device__ inline size_t mfh_c5_class_stride(int np_, int K)
     return (size_t)K * np_;
 }
 
-// class accumulators provably fit int32: a class has at most 3 (B8) or 1
-// (K7) digit products of np/64 rounds, each round at most K * 64 * 2^14
-static inline bool mfh_class_bound_ok(int K, int np_)
+// class accumulators provably fit int32: a class has at most `pairs` digit
+// products (3 for B8, 1 for K7) of np/64 rounds, each round at most
+// K * 64 * 2^14
+static inline bool mfh_class_bound_ok(int K, int np_, int pairs)
 {
-    return 3LL * (np_ / MFH_KBLK) * ((long long)K << 20) <= 2147483647LL;
+    return (long long)pairs * (np_ / MFH_KBLK) * ((long long)K << 20) <= 2147483647LL;
 }
 
 struct mfh_ctx {
@@ -90,6 +91,7 @@ struct mfh_ctx {
     int mode;             // digit mode of the current product (MFH_MODE_*)
     int recode;           // forward transform recodes limbs to signed form
     int k7_ok;            // plan admits MFH_MODE_K7 (workspace sized for it)
+    int b8_ok;            // size admits MFH_MODE_B8's int32 class bound
     int8_t *dAh, *dBh;    // digit planes [NB][K][planes][np][np]
     int32_t *dC5;         // pointwise class results (layout: mfh_c5_index)
     int64_t *dCw;         // coefficient planes [2L-1][n][n]

@@ -325,7 +325,9 @@ __device__ __forceinline__ void class_pairs(int m, int &rlo, int &npairs)
 //
 // Output: class m of (j, i, j', t) at mfh_c5_index + m * mfh_c5_class_stride.
 // Accumulator bound: a class has at most 3 digit pairs x np/64 rounds of at
-// most K * 2^20 each; mfh_create rejects sizes where that reaches 2^31.
+// most K * 2^20 each; mfh_create rejects sizes where that reaches 2^31 for
+// every digit mode the plan admits, and a product in a mode whose bound
+// fails is refused.
 template <class Cfg, int MODE>
 __global__ void __attribute__((amdgpu_flat_work_group_size(Cfg::THREADS, Cfg::THREADS),
                                amdgpu_waves_per_eu(Cfg::WPE, Cfg::WPE)))

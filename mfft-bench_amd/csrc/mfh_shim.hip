@@ -93,6 +93,7 @@ int run_conv(mfh_ctx *c, int kind, const void *dA, const void *dB, int64_t *Cw,
              int SA, int SB, uint16_t *out16 = nullptr, int RL = 0, int *carried = nullptr)
 {
     int rc;
+    if (c->mode == MFH_MODE_B8 && !c->b8_ok) return MFH_E_BOUND;
     mark(c, 0);
     const int eb = (kind == MFH_IN_U16 || kind == MFH_IN_U16_SIGNED) ? 2
                    : kind == MFH_IN_F64 ? 8 : 4;
@@ -166,7 +167,16 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     double bits = log2((double)p->NB) + log2((double)p->K) + log2((double)np_) +
                   2.0 * log2((double)(p->NB / 2) * 65535.0);
     if (bits >= 62.0) return MFH_E_BOUND;
-    if (!mfh_class_bound_ok(p->K, np_)) return MFH_E_BOUND;
+    // int32 classes: the 6-product mode (one product per class) admits 3x
+    // the size of the 9-product mode; a size only the former admits serves
+    // the products that use it (MFH_E_BOUND for the others, at call time)
+    mfh_ctx shape;
+    memset(&shape, 0, sizeof shape);
+    shape.n = n; shape.np = np_; shape.L = L; shape.S = p->S; shape.NB = p->NB; shape.K = p->K;
+    shape.use_fast = getenv("MFH_GENERIC_KERNELS") ? 0 : 1;
+    const bool k7_ok = k7_plain(&shape) || k7_recoded(&shape);
+    const bool b8_ok = mfh_class_bound_ok(p->K, np_, 3);
+    if (!b8_ok && !(k7_ok && mfh_class_bound_ok(p->K, np_, 1))) return MFH_E_BOUND;
     int rc = check_device();
     if (rc) return rc;
 
@@ -174,14 +184,15 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     memset(c, 0, sizeof *c);
     c->n = n; c->np = np_; c->L = L; c->S = p->S; c->NB = p->NB; c->K = p->K; c->g = p->g;
     c->dev = 0;
-    c->use_fast = getenv("MFH_GENERIC_KERNELS") ? 0 : 1;
+    c->use_fast = shape.use_fast;
+    c->b8_ok = b8_ok;
     if (hipSetDevice(0) != hipSuccess || hipStreamCreate(&c->stream) != hipSuccess) {
         delete c;
         return MFH_E_HIP;
     }
     for (int k = 0; k < 5; ++k) (void)hipEventCreate(&c->ev[k]);
     const size_t nnp = (size_t)np_ * np_, nn = (size_t)n * n;
-    c->k7_ok = k7_plain(c) || k7_recoded(c);
+    c->k7_ok = k7_ok;
     const int planes = c->k7_ok ? MFH_PLANES_MAX : MFH_DIGITS;
     const int classes = c->k7_ok ? MFH_CLASSES_MAX : MFH_CLASSES;
     select_mode(c, true);
@@ -228,9 +239,15 @@ int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut,
     return MFH_OK;
 }
 
+// products that return the caller's own limb convolution (conv_mfft, the
+// fixed-point floats) never recode, so they take the 6-product mode only
+// when plain K7 fits, else the 9-product mode and its class bound
+static bool conv_size_ok(const mfh_ctx *c) { return k7_plain(c) || c->b8_ok; }
+
 int mfh_conv_dev(mfh_ctx *c, const void *dA32, const void *dB32, void *dCw)
 {
     if (!c || !dA32 || !dB32 || !dCw) return MFH_E_ARG;
+    if (!conv_size_ok(c)) return MFH_E_BOUND;
     int rc, flag = 0;
     MFH_HIP(hipMemsetAsync(c->dFlag, 0, sizeof(int), c->stream));
     if ((rc = mfh_launch_check_i32(c, (const int32_t *)dA32, c->L))) return rc;
@@ -250,6 +267,7 @@ namespace {
 int fpx_mm_dev(mfh_ctx *c, int f64, const void *dA, const void *dB, int SA, int SB, void *dC)
 {
     if (!c || !dA || !dB || !dC) return MFH_E_ARG;
+    if (!conv_size_ok(c)) return MFH_E_BOUND;
     select_mode(c, false);
     int rc = run_conv(c, f64 ? MFH_IN_F64 : MFH_IN_F32, dA, dB, c->dCw, SA, SB);
     if (rc) return rc;
@@ -302,6 +320,7 @@ int mfh_mm(mfh_ctx *c, int kind, const uint16_t *A, const uint16_t *B, uint16_t 
 int mfh_conv(mfh_ctx *c, const int32_t *A32, const int32_t *B32, int64_t *Cw)
 {
     if (!c || !A32 || !B32 || !Cw) return MFH_E_ARG;
+    if (!conv_size_ok(c)) return MFH_E_BOUND;
     const size_t nn = (size_t)c->n * c->n;
     const size_t in_b = (size_t)c->L * nn * 4;
     const size_t out_b = (size_t)(2 * c->L - 1) * nn * 8;
@@ -319,6 +338,7 @@ namespace {
 int fpx_mm_host(mfh_ctx *c, int f64, const void *A, const void *B, int SA, int SB, void *C)
 {
     if (!c || !A || !B || !C) return MFH_E_ARG;
+    if (!conv_size_ok(c)) return MFH_E_BOUND;
     const size_t nn = (size_t)c->n * c->n, eb = f64 ? 8 : 4;
     int rc = ensure_staging(c, nn * eb, nn * eb);
     if (rc) return rc;

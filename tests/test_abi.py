@@ -113,10 +113,16 @@ def test_create_checks_arguments_and_bounds(lib):
     assert lib.mfh_create(C.byref(h), 64, 64, C.byref(p)) == -3         # L mismatch
     p1k = M.plan(1024)                                                  # K = 64
     assert lib.mfh_create(C.byref(h), 64, 1024, C.byref(p1k)) == -7
-    # int32 class accumulators: 3 * (np/64) * K * 2^20 must stay below 2^31
+    # int32 class accumulators: pairs * (np/64) * K * 2^20 must stay below
+    # 2^31 -- at K = 16 the 6-product mode (1 pair) admits n <= 8128
     assert lib.mfh_create(C.byref(h), 8192, 128, C.byref(p)) == -4
+    p64 = M.plan(64)                                   # NB = 16: plain 6-product digits
+    assert lib.mfh_create(C.byref(h), 8192, 64, C.byref(p64)) == -4
+    p512 = M.plan(512)                                 # K = 32, 9-product digits only
+    assert lib.mfh_create(C.byref(h), 1408, 512, C.byref(p512)) == -4
     if lib.mfh_device_count() == 0:
         assert lib.mfh_create(C.byref(h), 64, 128, C.byref(p)) == -1    # no device
+        assert lib.mfh_create(C.byref(h), 3072, 128, C.byref(p)) == -1  # past the bounds
         assert not h.value
 
 

@@ -353,6 +353,21 @@ def test_c5_n4096_w512_signed(gpu, orc, lib):
     check_large(gpu, orc, lib, 4096, 512, True)
 
 
+def test_n3072_w2048_beyond_the_9_product_bound(gpu, orc, lib):
+    """n = 3072 at 2048 bits: the exact track's 6-product digits keep the
+    int32 classes in range (the 9-product mode would not), so mm_mfft works;
+    conv_mfft, which must use 9-product digits at this plan, is refused."""
+    check_large(gpu, orc, lib, 3072, 2048, False)
+    n, L = 3072, 128
+    with gpu.Ctx(n, L) as ctx:
+        dA, dB = gpu.DevBuf(L * n * n * 4), gpu.DevBuf(L * n * n * 4)
+        dCw = gpu.DevBuf((2 * L - 1) * n * n * 8)
+        rc = lib.mfh_conv_dev(ctx.h, dA.ptr, dB.ptr, dCw.ptr)
+        for b in (dA, dB, dCw):
+            b.free()
+    assert rc == -4
+
+
 def test_c4_fp32_n2048(gpu, orc):
     n = 2048
     A = orc.fp32_rand(n * n, SEED, -20, 20)
