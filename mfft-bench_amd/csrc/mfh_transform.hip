@@ -256,8 +256,9 @@ __global__ __launch_bounds__(256) void k_forward_window(Src src, int8_t *__restr
 }
 
 // ---- forward transform, plan specialised at compile time ----------------------
-// One thread per element; the element's L limbs are held in registers (u16
-// pairs packed in one VGPR).  The NB output points are split into Q residue
+// One thread per element; the element's L limbs are staged in LDS (u16
+// pairs) for the workgroup's elements, or held in registers as int32 for
+// fixed-point floats.  The NB output points are split into Q residue
 // classes j = q + Q*j' (j' < P = NB/Q):
 //     X[q + Q j'] = sum_{b' < P} w^(j' b') z_q[b'],   w = omega^Q,
 //     z_q[b']     = sum_{b = b' mod P} omega^(q b) x_b
@@ -265,17 +266,6 @@ __global__ __launch_bounds__(256) void k_forward_window(Src src, int8_t *__restr
 // the L/S non-zero blocks into P), and each class is a length-P radix-2
 // DIF transform over K-vectors.  Every shift is a compile-time register
 // renaming; only additions and negations remain.
-template <int L>
-struct LimbsPacked {           // unsigned limbs, two per VGPR
-    uint32_t r[L / 2];
-    bool top_signed;
-    __device__ __forceinline__ int get(int u) const
-    {
-        const uint32_t w = r[u / 2];
-        if (u == L - 1 && top_signed) return (int)(short)(w >> 16);
-        return (u & 1) ? (int)(w >> 16) : (int)(w & 0xFFFFu);
-    }
-};
 template <int L>
 struct LimbsI32 {
     int r[L];
@@ -330,17 +320,6 @@ __device__ __forceinline__ void stage_limbs_u16(uint32_t *lds, const uint16_t *s
     }
 }
 
-template <int L, class Src>
-__device__ __forceinline__ void load_limbs(LimbsPacked<L> &x, const Src &src, int i, int k,
-                                           bool valid)
-{
-#pragma unroll
-    for (int u = 0; u < L; u += 2) {
-        uint32_t lo = valid ? (uint32_t)(uint16_t)src.get(u, i, k) : 0u;
-        uint32_t hi = valid ? (uint32_t)(uint16_t)src.get(u + 1, i, k) : 0u;
-        x.r[u / 2] = lo | (hi << 16);
-    }
-}
 template <int L, class Src>
 __device__ __forceinline__ void load_limbs(LimbsI32<L> &x, const Src &src, int i, int k,
                                            bool valid)
@@ -483,7 +462,6 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
         const int i = (int)(e / np_), k = (int)(e % np_);
         const bool valid = i < src.n && k < src.n;
         load_limbs<L>(x, src, i, k, valid);
-        if constexpr (std::is_same_v<Limbs, LimbsPacked<L>>) x.top_signed = top_signed != 0;
     }
     forward_parts<S, NB, Q, MODE, TPE, Limbs>(part, x, out + e, nnp);
 }
@@ -970,7 +948,7 @@ bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int top_signed)
            try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>>(c, s, dst, top_signed) ||  // W=1024
            try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst,   // W=8192
                                                                          top_signed) ||
-           try_fast<4, 16, K7, false, SrcU16, LimbsPacked<32>>(c, s, dst, top_signed); // W=512
+           try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>>(c, s, dst, top_signed);  // W=512
 }
 }  // namespace
 
