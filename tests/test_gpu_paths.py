@@ -88,11 +88,13 @@ def test_signed_entries(gpu, orc, n, L):
     assert err == 0 and np.array_equal(out, want)
 
 
-@pytest.mark.parametrize("RL", [1, 5, 64, 129])
-def test_short_and_long_outputs(gpu, orc, RL):
+@pytest.mark.parametrize("L,RL", [(64, 1), (64, 5), (64, 64), (64, 129), (32, 3), (32, 70),
+                                  (128, 2), (128, 100), (128, 262), (512, 1), (512, 37),
+                                  (512, 1030)])
+def test_short_and_long_outputs(gpu, orc, L, RL):
     """RL below 2L+1 truncates mod 2^(16 RL), above it zero-extends
-    (src/bigmat.c:48-60)."""
-    n, L = 16, 64
+    (src/bigmat.c:48-60); every ring size, so every fused-carry layout."""
+    n = 16
     A = orc.bigmat_rand(n, L, 3)
     B = orc.bigmat_rand(n, L, 4)
     want = orc.normalize(orc.conv_limbplane(A.astype(np.int32), B.astype(np.int32), n, L),
