@@ -69,6 +69,15 @@ int  mfh_create(mfh_ctx **ctx, int n, int L, const mfh_plan *plan);
 void mfh_destroy(mfh_ctx *ctx);
 /* device bytes held by the context */
 size_t mfh_workspace_bytes(const mfh_ctx *ctx);
+/* Row band height of the context's products (no reference counterpart: the
+ * reference holds every transformed operand in host memory).  A's
+ * transformed digits and the pointwise results are held for this many
+ * padded rows at a time; it is n rounded up to a multiple of 64 (one band)
+ * when the whole workspace fits in 90 % of the device memory free at
+ * mfh_create, else the largest multiple of 64 rows that does, at least
+ * 1/64 of the rows (MFH_E_NOMEM below that).  The environment variable
+ * MFH_BAND_ROWS=<rows>, read at mfh_create, forces a height. */
+int  mfh_band_rows(const mfh_ctx *ctx);
 
 /* ---- host-buffer entry points (synchronous) ----------------------------- */
 /* mm_mfft: exact product of unsigned (or, with MFH_IN_U16_SIGNED, two's

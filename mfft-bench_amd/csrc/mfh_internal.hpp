@@ -55,17 +55,18 @@ static inline int mfh_nclasses(int mode) { return mode == MFH_MODE_K7 ? 6 : 5; }
 
 #define MFH_CLASSES (2 * MFH_DIGITS - 1)
 
-// Layout of the pointwise step's int32 class results: for point j, element
-// (i, j'), class m and ring coefficient t = 4q + r, with j' = 16 jb + jl,
+// Layout of the pointwise step's int32 class results for a band of `rows`
+// padded rows of A: for point j, element (i, j') with i the row within the
+// band, class m and ring coefficient t = 4q + r, with j' = 16 jb + jl,
 //     C5[j][i][m][jb][q][jl][r]       (q < K/4, r < 4, jl < 16)
 // One wave's store of 4 consecutive t of 16 consecutive j' is then 256
 // contiguous bytes, and the K values of 16 consecutive elements lie in one
 // K*64-byte run.  Index of class 0 of (j, i, j', t); classes are
 // mfh_c5_class_stride(np, K) ints apart.
 __host__ __device__ inline size_t mfh_c5_index(int j, int i, int jj, int t, int np_, int ncl,
-                                               int K)
+                                               int K, int rows)
 {
-    const size_t row = ((size_t)j * np_ + i) * ncl;            // class 0 of (j, i)
+    const size_t row = ((size_t)j * rows + i) * ncl;           // class 0 of (j, i)
     return ((row * (np_ / 16) + jj / 16) * (K / 4) + t / 4) * 64 + (jj & 15) * 4 + (t & 3);
 }
 __host__ __device__ inline size_t mfh_c5_class_stride(int np_, int K)
@@ -81,6 +82,10 @@ static inline bool mfh_class_bound_ok(int K, int np_, int pairs)
     return (long long)pairs * (np_ / MFH_KBLK) * ((long long)K << 20) <= 2147483647LL;
 }
 
+// at most this many row bands per product (the band height is at least
+// np / MFH_BANDS_MAX rows)
+#define MFH_BANDS_MAX 64
+
 struct mfh_ctx {
     int n, np;            // matrix size, padded to a multiple of 64
     int L, S, NB, K, g;
@@ -92,8 +97,11 @@ struct mfh_ctx {
     int recode;           // forward transform recodes limbs to signed form
     int k7_ok;            // plan admits MFH_MODE_K7 (workspace sized for it)
     int b8_ok;            // size admits MFH_MODE_B8's int32 class bound
-    int8_t *dAh, *dBh;    // digit planes [NB][K][planes][np][np]
-    int32_t *dC5;         // pointwise class results (layout: mfh_c5_index)
+    int hb;               // row band height: A's digit planes and the class
+                          // results hold hb padded rows at a time
+    int8_t *dAh;          // A's digit planes [NB][K][planes][hb][np]
+    int8_t *dBh;          // B's digit planes [NB][K][planes][np][np]
+    int32_t *dC5;         // pointwise class results of a band (mfh_c5_index)
     int64_t *dCw;         // coefficient planes [2L-1][n][n]
     void *dBt;            // transposed B input, up to L*n*n int32
     int *dFlag;           // device error flags
@@ -104,22 +112,32 @@ struct mfh_ctx {
     // last product: output kind (0 limbs, 1 coefficient planes, 2 fp32),
     // output limbs, whether the carry ran inside the inverse kernel
     int last_out, last_RL, last_fused;
-    // timing
+    // timing: ev[0] start, ev[4] end; per row band b, bev[b][0..3] before
+    // A's forward transform, after it, after the pointwise step, after the
+    // inverse (nbands of them)
     int timing;
+    int nbands;
     hipEvent_t ev[5];
+    hipEvent_t bev[MFH_BANDS_MAX][4];
     float stage_ms[5];
 };
 
 // kernel launchers (mfh_transform.hip, mfh_pointwise.hip)
 int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
                          int elem_bytes, hipStream_t st);
+// Row bands: the forward transform of padded rows [r0, r0 + rows) of an
+// operand (digit planes of rows x np), the pointwise products of A's band
+// with all of B, and the inverse of the band's elements (rows r0.. below n,
+// written at their places in the n x n outputs).  rows is a multiple of 64,
+// or reaches np.
 int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
-                       int scale_S);
+                       int scale_S, int r0, int rows);
 int mfh_launch_check_i32(mfh_ctx *c, const int32_t *src, int planes);
-int mfh_launch_pointwise(mfh_ctx *c);
+int mfh_launch_pointwise(mfh_ctx *c, int rows);
 // out != nullptr asks for the carry into RL uint16 limbs to be fused;
 // *carried tells whether it was (else Cw holds the coefficient planes)
-int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carried);
+int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carried, int r0,
+                       int rows);
 int mfh_launch_carry(mfh_ctx *c, const int64_t *Cw, uint16_t *out, int RL);
 int mfh_launch_carry_planes(const int64_t *Cw, int P, size_t nn, uint16_t *out,
                             int RL, hipStream_t st);

@@ -26,9 +26,10 @@
 // suffices; the orientation of the accumulator (+(P-N) or -(P-N)) is known
 // from the direction of the last round and applied at the flush.
 //
-// Operands in HBM: digit plane (j, c, r) is an np x np int8 matrix,
-// row-major with the reduction index k contiguous (A as A[i][k], B stored
-// transposed as B^T[j'][k]).  Each round stages, for all K ring
+// Operands in HBM: digit plane (j, c, r) is an int8 matrix, row-major with
+// the reduction index k contiguous (A as A[i][k], B stored transposed as
+// B^T[j'][k]); B's planes hold all np rows, A's the `rows` rows of the
+// current row band.  Each round stages, for all K ring
 // coefficients, a (16*WBI) x 64 tile of A and a (16*WBJ) x 64 tile of B^T
 // into LDS in MFMA operand order (lane l of a 16x64 fragment = row l%16,
 // k bytes 16*(l/16) .. +15; A and B use the same k order, so the dot
@@ -332,7 +333,7 @@ template <class Cfg, int MODE>
 __global__ void __attribute__((amdgpu_flat_work_group_size(Cfg::THREADS, Cfg::THREADS),
                                amdgpu_waves_per_eu(Cfg::WPE, Cfg::WPE)))
 k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
-            int32_t *__restrict__ C5, int np_, int tiles_j)
+            int32_t *__restrict__ C5, int np_, int rows, int tiles_j)
 {
     constexpr int K = Cfg::K, T = Cfg::T, WBI = Cfg::WBI, WBJ = Cfg::WBJ, W = Cfg::WAVES;
     constexpr int NCLASS = MODE == MFH_MODE_K7 ? 6 : 2 * MFH_DIGITS - 1;
@@ -351,20 +352,21 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     int ti, tj, jp;
     tile_of(tiles_j, ti, tj, jp);
     const int i0 = ti * Cfg::BI, j0 = tj * Cfg::BJ;
-    const size_t plane = (size_t)np_ * np_;
-    const int8_t *Aj = Ah + (size_t)jp * K * PL * plane;
+    const size_t plane = (size_t)np_ * np_;           // B: all np rows
+    const size_t planeA = (size_t)rows * np_;         // A: the band's rows
+    const int8_t *Aj = Ah + (size_t)jp * K * PL * planeA;
     const int8_t *Bj = Bh + (size_t)jp * K * PL * plane;
 
     // this wave's fragments f = wave + W*i:
     //   A: coefficient f / WBI, row block f % WBI
     //   B: coefficient f / WBJ, column block f % WBJ
-    const int8_t *a_blk = Aj + (size_t)(wave / WBI) * PL * plane +
+    const int8_t *a_blk = Aj + (size_t)(wave / WBI) * PL * planeA +
                           (size_t)(i0 + (wave % WBI) * 16) * np_ +
                           (lane & 15) * np_ + (lane >> 4) * 16;
     const int8_t *b_blk = Bj + (size_t)(wave / WBJ) * PL * plane +
                           (size_t)(j0 + (wave % WBJ) * 16) * np_ +
                           (lane & 15) * np_ + (lane >> 4) * 16;
-    const size_t da = (size_t)(W / WBI) * PL * plane;
+    const size_t da = (size_t)(W / WBI) * PL * planeA;
     const size_t db = (size_t)(W / WBJ) * PL * plane;
     v4i *wa = lds + wave * 64 + lane;                     // this lane's A slot of fragment f=wave
     v4i *wbp = lds + Cfg::A_CHUNKS + wave * 64 + lane;
@@ -379,7 +381,7 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     // copy fills (DMA mode): the round's A or B tiles straight into LDS
     auto srcs = [&](RoundPos q, const int8_t *&a0, const int8_t *&b0) {
         const int s = MODE == MFH_MODE_K7 ? q.r : q.m - q.r;
-        a0 = a_blk + (size_t)q.r * plane + q.kb * MFH_KBLK;
+        a0 = a_blk + (size_t)q.r * planeA + q.kb * MFH_KBLK;
         b0 = b_blk + (size_t)s * plane + q.kb * MFH_KBLK;
     };
     auto dma_a = [&](RoundPos q) {
@@ -404,7 +406,7 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
         const int s = MODE == MFH_MODE_K7 ? r : q.m - r;
 #pragma unroll
         for (int sb = 0; sb < KB; ++sb) {
-            const int8_t *a0 = a_blk + (size_t)r * plane + (kb * KB + sb) * MFH_KBLK;
+            const int8_t *a0 = a_blk + (size_t)r * planeA + (kb * KB + sb) * MFH_KBLK;
             const int8_t *b0 = b_blk + (size_t)s * plane + (kb * KB + sb) * MFH_KBLK;
 #pragma unroll
             for (int i = 0; i < NA; ++i) R[sb * NF + i] = *(const v4i *)(a0 + i * da);
@@ -540,7 +542,8 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
                 // read once, by the inverse transform: stream past the caches
                 const v4i qv = {q.x, q.y, q.z, q.w};
                 __builtin_nontemporal_store(
-                    qv, (v4i *)(C5 + mfh_c5_index(jp, row0 + v, col, tg * T + tt, np_, NCLASS, K) +
+                    qv, (v4i *)(C5 + mfh_c5_index(jp, row0 + v, col, tg * T + tt, np_, NCLASS, K,
+                                                 rows) +
                                 (size_t)m * mfh_c5_class_stride(np_, K)));
             }
         }
@@ -548,11 +551,12 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
 }
 
 template <class Cfg>
-int launch_cfg(mfh_ctx *c)
+int launch_cfg(mfh_ctx *c, int rows)
 {
-    if (c->np % (MFH_KBLK * Cfg::KB) || c->np % Cfg::BI || c->np % Cfg::BJ)
+    if (c->np % (MFH_KBLK * Cfg::KB) || rows % Cfg::BI || c->np % Cfg::BJ || rows < 1 ||
+        rows > c->np)
         return MFH_E_UNSUPPORTED;
-    const int tiles_i = c->np / Cfg::BI, tiles_j = c->np / Cfg::BJ;
+    const int tiles_i = rows / Cfg::BI, tiles_j = c->np / Cfg::BJ;
     static bool attr_set = false;
     if (!attr_set) {
         MFH_HIP(hipFuncSetAttribute((const void *)k_pointwise<Cfg, MFH_MODE_B8>,
@@ -566,20 +570,22 @@ int launch_cfg(mfh_ctx *c)
     dim3 grid((unsigned)(tiles_i * tiles_j), (unsigned)c->NB);
     if (c->mode == MFH_MODE_K7)
         hipLaunchKernelGGL((k_pointwise<Cfg, MFH_MODE_K7>), grid, dim3(Cfg::THREADS),
-                           Cfg::DYN_LDS, c->stream, c->dAh, c->dBh, c->dC5, c->np, tiles_j);
+                           Cfg::DYN_LDS, c->stream, c->dAh, c->dBh, c->dC5, c->np, rows,
+                           tiles_j);
     else
         hipLaunchKernelGGL((k_pointwise<Cfg, MFH_MODE_B8>), grid, dim3(Cfg::THREADS),
-                           Cfg::DYN_LDS, c->stream, c->dAh, c->dBh, c->dC5, c->np, tiles_j);
+                           Cfg::DYN_LDS, c->stream, c->dAh, c->dBh, c->dC5, c->np, rows,
+                           tiles_j);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }
 
 }  // namespace
 
-int mfh_launch_pointwise(mfh_ctx *c)
+int mfh_launch_pointwise(mfh_ctx *c, int rows)
 {
     switch (c->K) {
-    case 4:  return launch_cfg<PwCfg<4, 4, 2, 2>>(c);
+    case 4:  return launch_cfg<PwCfg<4, 4, 2, 2>>(c, rows);
     // K = 8 and K = 16: copy fills with the B fragments held in registers,
     // one workgroup per CU (64 x 64 tiles, 16 waves at 4 per SIMD, 116
     // VGPRs; 64 x 32 tiles, 8 waves at 2 per SIMD, 214 VGPRs): measured
@@ -587,12 +593,12 @@ int mfh_launch_pointwise(mfh_ctx *c)
     // with half the tile.  For K = 16 the barrier and the copies come after
     // the round's third step of MFMAs, so the MFMAs start as soon as this
     // wave's fragments are in (another 4 %; for K = 8 it is slower).
-    case 8:  return launch_cfg<PwCfg<8, 8, 4, 4, 1, 4, true, 1>>(c);
-    case 16: return launch_cfg<PwCfg<16, 16, 4, 2, 1, 2, true, 4>>(c);
+    case 8:  return launch_cfg<PwCfg<8, 8, 4, 4, 1, 4, true, 1>>(c, rows);
+    case 16: return launch_cfg<PwCfg<16, 16, 4, 2, 1, 2, true, 4>>(c, rows);
     // K = 32: the same with one 4-wave workgroup per CU at one wave per
     // SIMD (fragments and accumulators need 256 VGPRs + 214 AGPRs; 6 %
     // faster than 8-coefficient waves with a sliding A window)
-    case 32: return launch_cfg<PwCfg<32, 32, 2, 2, 1, 1, true, 1>>(c);
+    case 32: return launch_cfg<PwCfg<32, 32, 2, 2, 1, 1, true, 1>>(c, rows);
     default: return MFH_E_UNSUPPORTED;
     }
 }

@@ -85,10 +85,17 @@ void mark(mfh_ctx *c, int k)
 {
     if (c->timing) (void)hipEventRecord(c->ev[k], c->stream);
 }
+void mark_band(mfh_ctx *c, int b, int k)
+{
+    if (c->timing) (void)hipEventRecord(c->bev[b][k], c->stream);
+}
 
 // transforms in, pointwise, inverse; leaves the coefficient planes in Cw,
 // or, when out16 is given and the inverse kernel fuses the carry, the RL
-// output limbs in out16 (*carried = 1)
+// output limbs in out16 (*carried = 1).  B is transformed once; A goes
+// through in row bands of c->hb padded rows (one band when the whole
+// workspace fits), each transformed, multiplied by all of B and inverted
+// into its rows of the output.
 int run_conv(mfh_ctx *c, int kind, const void *dA, const void *dB, int64_t *Cw,
              int SA, int SB, uint16_t *out16 = nullptr, int RL = 0, int *carried = nullptr)
 {
@@ -99,15 +106,45 @@ int run_conv(mfh_ctx *c, int kind, const void *dA, const void *dB, int64_t *Cw,
                    : kind == MFH_IN_F64 ? 8 : 4;
     const int planes = (kind == MFH_IN_F32 || kind == MFH_IN_F64) ? 1 : c->L;
     if ((rc = mfh_launch_transpose(dB, c->dBt, planes, c->n, eb, c->stream))) return rc;
-    if ((rc = mfh_launch_forward(c, kind, dA, c->dAh, SA))) return rc;
-    if ((rc = mfh_launch_forward(c, kind, c->dBt, c->dBh, SB))) return rc;
-    mark(c, 1);
-    if ((rc = mfh_launch_pointwise(c))) return rc;
-    mark(c, 2);
-    int fused = 0;
-    if ((rc = mfh_launch_inverse(c, Cw, out16, RL, &fused))) return rc;
+    if ((rc = mfh_launch_forward(c, kind, c->dBt, c->dBh, SB, 0, c->np))) return rc;
+    int fused = 0, b = 0;
+    for (int r0 = 0; r0 < c->n; r0 += c->hb, ++b) {
+        const int rows = c->hb < c->np - r0 ? c->hb : c->np - r0;
+        mark_band(c, b, 0);
+        if ((rc = mfh_launch_forward(c, kind, dA, c->dAh, SA, r0, rows))) return rc;
+        mark_band(c, b, 1);
+        if ((rc = mfh_launch_pointwise(c, rows))) return rc;
+        mark_band(c, b, 2);
+        if ((rc = mfh_launch_inverse(c, Cw, out16, RL, &fused, r0, rows))) return rc;
+        mark_band(c, b, 3);
+    }
     if (carried) *carried = fused;
-    mark(c, 3);
+    return MFH_OK;
+}
+
+// Row band height: all np rows when A's digit planes, B's, the class
+// results and the fixed buffers fit in 90 % of the device memory free now,
+// else the most multiples of 64 rows that do (at least np / MFH_BANDS_MAX).
+// MFH_BAND_ROWS=<rows> forces a height (rounded up to a multiple of 64).
+int band_rows(int np_, size_t per_row, size_t fixed, int *hb)
+{
+    const int min_rows = ((np_ + MFH_BANDS_MAX - 1) / MFH_BANDS_MAX + 63) / 64 * 64;
+    if (const char *env = getenv("MFH_BAND_ROWS")) {
+        long v = strtol(env, nullptr, 10);
+        if (v > 0) {
+            long r = (v + 63) / 64 * 64;
+            if (r < min_rows) r = min_rows;
+            *hb = r < np_ ? (int)r : np_;
+            return MFH_OK;
+        }
+    }
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return MFH_E_HIP;
+    const double budget = 0.9 * (double)free_b - (double)fixed;
+    if ((double)per_row * np_ <= budget) { *hb = np_; return MFH_OK; }
+    const long fit = budget > 0 ? (long)(budget / (double)per_row) / 64 * 64 : 0;
+    if (fit < min_rows) return MFH_E_NOMEM;
+    *hb = (int)fit;
     return MFH_OK;
 }
 
@@ -196,13 +233,21 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     const int planes = c->k7_ok ? MFH_PLANES_MAX : MFH_DIGITS;
     const int classes = c->k7_ok ? MFH_CLASSES_MAX : MFH_CLASSES;
     select_mode(c, true);
-    const size_t digit_bytes = (size_t)c->NB * c->K * planes * nnp;
-    rc = dalloc(c, (void **)&c->dAh, digit_bytes);
-    if (!rc) rc = dalloc(c, (void **)&c->dBh, digit_bytes);
-    if (!rc) rc = dalloc(c, (void **)&c->dC5,
-                         (size_t)c->NB * classes * c->K * nnp * sizeof(int32_t));
-    if (!rc) rc = dalloc(c, (void **)&c->dCw, (size_t)(2 * L - 1) * nn * sizeof(int64_t));
-    if (!rc) rc = dalloc(c, &c->dBt, (size_t)L * nn * sizeof(int32_t));
+    // per padded row of A: its digit planes and its class results
+    const size_t digit_row = (size_t)c->NB * c->K * planes * np_;
+    const size_t c5_row = (size_t)c->NB * classes * c->K * np_ * sizeof(int32_t);
+    const size_t cw_bytes = (size_t)(2 * L - 1) * nn * sizeof(int64_t);
+    const size_t bt_bytes = (size_t)L * nn * sizeof(int32_t);
+    rc = band_rows(np_, digit_row + c5_row, digit_row * np_ + cw_bytes + bt_bytes, &c->hb);
+    if (rc) { mfh_destroy(c); return rc; }
+    c->nbands = (n + c->hb - 1) / c->hb;
+    for (int b = 0; b < c->nbands; ++b)
+        for (int k = 0; k < 4; ++k) (void)hipEventCreate(&c->bev[b][k]);
+    rc = dalloc(c, (void **)&c->dAh, digit_row * c->hb);
+    if (!rc) rc = dalloc(c, (void **)&c->dBh, digit_row * np_);
+    if (!rc) rc = dalloc(c, (void **)&c->dC5, c5_row * c->hb);
+    if (!rc) rc = dalloc(c, (void **)&c->dCw, cw_bytes);
+    if (!rc) rc = dalloc(c, &c->dBt, bt_bytes);
     if (!rc) rc = dalloc(c, (void **)&c->dFlag, sizeof(int));
     if (rc) { mfh_destroy(c); return rc; }
     *out = c;
@@ -219,11 +264,15 @@ void mfh_destroy(mfh_ctx *c)
         if (b) (void)hipFree(b);
     for (int k = 0; k < 5; ++k)
         if (c->ev[k]) (void)hipEventDestroy(c->ev[k]);
+    for (int b = 0; b < c->nbands; ++b)
+        for (int k = 0; k < 4; ++k)
+            if (c->bev[b][k]) (void)hipEventDestroy(c->bev[b][k]);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
 
 size_t mfh_workspace_bytes(const mfh_ctx *c) { return c ? c->bytes : 0; }
+int mfh_band_rows(const mfh_ctx *c) { return c ? c->hb : MFH_E_ARG; }
 
 int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut, int RL)
 {
@@ -426,7 +475,17 @@ int mfh_stage_times(const mfh_ctx *c, float ms[5])
 {
     if (!c || !ms) return MFH_E_ARG;
     MFH_HIP(hipEventSynchronize(c->ev[4]));
-    for (int k = 0; k < 4; ++k) MFH_HIP(hipEventElapsedTime(&ms[k], c->ev[k], c->ev[k + 1]));
+    // transforms in: B's (up to band 0) and every band's A; each band's
+    // pointwise and inverse; carry/decode after the last band
+    float t = 0;
+    MFH_HIP(hipEventElapsedTime(&ms[0], c->ev[0], c->bev[0][0]));
+    ms[1] = ms[2] = 0;
+    for (int b = 0; b < c->nbands; ++b)
+        for (int k = 0; k < 3; ++k) {
+            MFH_HIP(hipEventElapsedTime(&t, c->bev[b][k], c->bev[b][k + 1]));
+            ms[k] += t;
+        }
+    MFH_HIP(hipEventElapsedTime(&ms[3], c->bev[c->nbands - 1][3], c->ev[4]));
     MFH_HIP(hipEventElapsedTime(&ms[4], c->ev[0], c->ev[4]));
     return MFH_OK;
 }

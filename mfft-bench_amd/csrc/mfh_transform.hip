@@ -182,19 +182,21 @@ __device__ __forceinline__ void store_digits(int8_t *p, size_t nnp, int v)
 }
 
 // ---- forward transform, generic plan ---------------------------------------
-// One thread per padded element (i, k) of an np x np operand; it writes the
-// three digit planes of every (point j, coefficient c).  Elements outside
-// the n x n input are zero.  Output plane (j, c, r) holds digit r of X[j][c]
-// as an np x np row-major int8 matrix.
+// One thread per padded element (i, k) of a band of `rows` padded rows from
+// row0 of an np x np operand; it writes the digit planes of every (point j,
+// coefficient c).  Elements outside the n x n input are zero.  Output plane
+// (j, c, r) holds digit r of X[j][c] as a rows x np row-major int8 matrix
+// (the whole operand when row0 = 0, rows = np; the other forward kernels
+// take the same band).
 template <class Src, int MODE>
 __global__ __launch_bounds__(256) void k_forward_generic(
     Src src, int8_t *__restrict__ out, int np_, int LS, int S, int NB, int K,
-    int g)
+    int g, int row0, int rows)
 {
-    const size_t nnp = (size_t)np_ * np_;
+    const size_t nnp = (size_t)rows * np_;         // the band's elements (plane stride)
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= nnp) return;
-    const int i = (int)(e / np_), k = (int)(e % np_);
+    const int i = row0 + (int)(e / np_), k = (int)(e % np_);
     const bool valid = i < src.n && k < src.n;
     const int twoK = 2 * K;
     for (int j = 0; j < NB; ++j) {
@@ -223,13 +225,14 @@ __global__ __launch_bounds__(256) void k_forward_generic(
 // encoder drops them (src/fpfixed.c:155-156).
 template <class Src, int MODE>
 __global__ __launch_bounds__(256) void k_forward_window(Src src, int8_t *__restrict__ out,
-                                                        int np_, int S, int NB, int K, int g)
+                                                        int np_, int S, int NB, int K, int g,
+                                                        int row0, int rows)
 {
     constexpr int NW = Src::NW;
-    const size_t nnp = (size_t)np_ * np_;
+    const size_t nnp = (size_t)rows * np_;
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= nnp) return;
-    const int i = (int)(e / np_), k = (int)(e % np_);
+    const int i = row0 + (int)(e / np_), k = (int)(e % np_);
     int lo = src.L, r[NW];
     if (i < src.n && k < src.n) src.window(i, k, lo, r);
     int b[NW], s[NW];
@@ -413,13 +416,14 @@ __device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *
 // E elements per workgroup of 256 threads, 256/E threads per element.
 template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src, int E = 256>
 __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restrict__ out, int np_,
-                                                      int top_signed)
+                                                      int top_signed, int row0, int rows)
 {
     constexpr int L = NB * S / 2;
     constexpr int TPE = 256 / E;
     static_assert(E * TPE == 256 && Q % TPE == 0, "threads split evenly over classes");
     static_assert(!RECODE || TPE == 1, "recoding rewrites the staged limbs in place");
-    const size_t nnp = (size_t)np_ * np_;
+    const size_t nnp = (size_t)rows * np_;           // the band's elements (plane stride)
+    const size_t eband = (size_t)row0 * np_;         // its first element in the operand
     const size_t e0 = (size_t)blockIdx.x * E;
     const int slot = threadIdx.x % E;
     const int part = __builtin_amdgcn_readfirstlane(threadIdx.x / E);
@@ -427,7 +431,7 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
     Limbs x;
     if constexpr (std::is_same_v<Limbs, LimbsLds<L, E>>) {
         __shared__ uint32_t stage[(L / 2) * E];
-        stage_limbs_u16<L, E>(stage, src.p, src.n, src.nn, np_, e0);
+        stage_limbs_u16<L, E>(stage, src.p, src.n, src.nn, np_, eband + e0);
         __syncthreads();
         x.base = stage + slot;
         x.top_signed = top_signed != 0;
@@ -459,7 +463,7 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
         if (e >= nnp) return;
     } else {
         if (e >= nnp) return;
-        const int i = (int)(e / np_), k = (int)(e % np_);
+        const int i = row0 + (int)(e / np_), k = (int)(e % np_);
         const bool valid = i < src.n && k < src.n;
         load_limbs<L>(x, src, i, k, valid);
     }
@@ -487,25 +491,28 @@ __global__ __launch_bounds__(256) void k_check_i32(const int32_t *p, size_t coun
 // Cooley-Tukey stages len = 2..NB with conjugate twiddles give NB * x_b in
 // natural order (the semantics of src/mfft.c:260-299).  Fold:
 //     Cw[b*S + c] = x_b[c] + x_(b-1)[c + S],  c < S   (src/mfft.c:407-418)
+// The elements are those of rows r0.. of a row band ([eb0, eb1) of the n x n
+// matrix); the class results hold the band's `rows` padded rows.
 __global__ void k_inverse_fold(const int32_t *__restrict__ C5,
                                int64_t *__restrict__ Cw, int n, int np_,
                                int NB, int K, int S, int g, int lgNB, int P,
-                               int epw, int mode, int ncl)
+                               int epw, int mode, int ncl, size_t eb0, size_t eb1, int r0,
+                               int rows)
 {
     extern __shared__ int64_t sm[];
     const int tid = threadIdx.x;
     const int le = tid / K, c = tid % K;
     const size_t nn = (size_t)n * n;
-    const size_t e = (size_t)blockIdx.x * epw + le;
-    const bool valid = le < epw && e < nn;
+    const size_t e = eb0 + (size_t)blockIdx.x * epw + le;
+    const bool valid = le < epw && e < eb1;
     const int blk = NB * K;
     int64_t *X = sm + (size_t)le * blk;
     int64_t *Y = sm + (size_t)epw * blk + (size_t)le * blk;
-    const int i = valid ? (int)(e / n) : 0, jj = valid ? (int)(e % n) : 0;
+    const int i = valid ? (int)(e / n) - r0 : 0, jj = valid ? (int)(e % n) : 0;
     if (valid) {
         for (int j = 0; j < NB; ++j) {
             const int r = lgNB ? (int)(__brev((unsigned)j) >> (32 - lgNB)) : 0;
-            X[r * K + c] = combine_classes(C5 + mfh_c5_index(j, i, jj, c, np_, ncl, K),
+            X[r * K + c] = combine_classes(C5 + mfh_c5_index(j, i, jj, c, np_, ncl, K, rows),
                                            mfh_c5_class_stride(np_, K), mode);
         }
     }
@@ -566,7 +573,8 @@ template <int NB, int K, bool CARRY, int NPASS = 2>
 __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict__ C5,
                                                       int64_t *__restrict__ Cw,
                                                       uint16_t *__restrict__ out, int RL,
-                                                      int n, int np_, int P, int mode, int ncl)
+                                                      int n, int np_, int P, int mode, int ncl,
+                                                      size_t eb0, size_t eb1, int r0, int rows)
 {
     constexpr int S = K / 2, g = 2 * K / NB, twoK = 2 * K;
     constexpr int PASS = 256 / K;            // elements per pass
@@ -577,13 +585,13 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
     const int c = lane % K;
     const int gbase = (lane / K) * K;        // first lane of this element's group
     const size_t nn = (size_t)n * n;
-    const size_t e0 = (size_t)blockIdx.x * E;
+    const size_t e0 = eb0 + (size_t)blockIdx.x * E;      // elements [eb0, eb1): a row band
 #pragma unroll
     for (int pass = 0; pass < NPASS; ++pass) {
         const int el = pass * PASS + tid / K;
         const size_t e = e0 + el;
-        const bool valid = e < nn;
-        const int i = valid ? (int)(e / n) : 0, jj = valid ? (int)(e % n) : 0;
+        const bool valid = e < eb1;
+        const int i = valid ? (int)(e / n) - r0 : 0, jj = valid ? (int)(e % n) : 0;
         long long X[NB];
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
@@ -591,7 +599,7 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
 #pragma unroll
             for (int bit = 1, rb = NB >> 1; bit < NB; bit <<= 1, rb >>= 1)
                 if (j & bit) r |= rb;
-            X[r] = valid ? combine_classes(C5 + mfh_c5_index(j, i, jj, c, np_, ncl, K),
+            X[r] = valid ? combine_classes(C5 + mfh_c5_index(j, i, jj, c, np_, ncl, K, rows),
                                            mfh_c5_class_stride(np_, K), mode)
                          : 0;
         }
@@ -625,7 +633,7 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
         }
     }
     __syncthreads();
-    const int ecount = (int)((nn - e0) < (size_t)E ? (nn - e0) : (size_t)E);
+    const int ecount = (int)((eb1 - e0) < (size_t)E ? (eb1 - e0) : (size_t)E);
     if constexpr (CARRY) {
         // Carry over the RL output limbs by SEGS = 256/E threads per element,
         // each owning a run of `len` >= 4 consecutive limbs (carry lookahead):
@@ -929,55 +937,55 @@ namespace {
 // compile-time plans: (S, NB) with Q output classes of length NB/Q
 template <int S, int NB, int MODE, bool RECODE, class Src, class Limbs, int E = 256,
           int Q = NB / 4>
-bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_signed)
+bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_signed, int row0, int rows)
 {
     if (c->S != S || c->NB != NB || c->mode != MODE || (c->recode != 0) != RECODE) return false;
-    const size_t nnp = (size_t)c->np * c->np;
+    const size_t nnp = (size_t)rows * c->np;
     hipLaunchKernelGGL((k_forward_fast<S, NB, Q, MODE, RECODE, Limbs, Src, E>),
                        dim3((unsigned)((nnp + E - 1) / E)), dim3(256), 0, c->stream, s, dst,
-                       c->np, top_signed);
+                       c->np, top_signed, row0, rows);
     return true;
 }
 
-bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int top_signed)
+bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, int rows)
 {
     constexpr int K7 = MFH_MODE_K7, B8 = MFH_MODE_B8;
     if (c->n % 8) return false;   // staged 16-byte loads need rows of 8k limbs
-    return try_fast<8, 32, K7, true, SrcU16, LimbsLds<128>>(c, s, dst, top_signed) ||  // W=2048
-           try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>>(c, s, dst, top_signed) ||
-           try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>>(c, s, dst, top_signed) ||  // W=1024
-           try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst,   // W=8192
-                                                                         top_signed) ||
-           try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>>(c, s, dst, top_signed);  // W=512
+    return try_fast<8, 32, K7, true, SrcU16, LimbsLds<128>>(c, s, dst, ts, r0, rows) ||  // W=2048
+           try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>>(c, s, dst, ts, r0, rows) ||
+           try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>>(c, s, dst, ts, r0, rows) ||  // W=1024
+           try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst, ts, r0,
+                                                                         rows) ||   // W=8192
+           try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>>(c, s, dst, ts, r0, rows);  // W=512
 }
 }  // namespace
 
 template <class Src>
-void launch_generic(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid, int LS)
+void launch_generic(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid, int LS, int r0, int rows)
 {
     if (c->mode == MFH_MODE_K7)
         hipLaunchKernelGGL((k_forward_generic<Src, MFH_MODE_K7>), grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g, r0, rows);
     else
         hipLaunchKernelGGL((k_forward_generic<Src, MFH_MODE_B8>), grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g);
+                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g, r0, rows);
 }
 
 template <class Src>
-void launch_window(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid)
+void launch_window(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid, int r0, int rows)
 {
     if (c->mode == MFH_MODE_K7)
         hipLaunchKernelGGL((k_forward_window<Src, MFH_MODE_K7>), grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, c->S, c->NB, c->K, c->g);
+                           s, dst, c->np, c->S, c->NB, c->K, c->g, r0, rows);
     else
         hipLaunchKernelGGL((k_forward_window<Src, MFH_MODE_B8>), grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, c->S, c->NB, c->K, c->g);
+                           s, dst, c->np, c->S, c->NB, c->K, c->g, r0, rows);
 }
 
 int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
-                       int scale_S)
+                       int scale_S, int r0, int rows)
 {
-    const size_t nnp = (size_t)c->np * c->np;
+    const size_t nnp = (size_t)rows * c->np;
     const size_t nn = (size_t)c->n * c->n;
     dim3 grid((unsigned)((nnp + 255) / 256));
     const int LS = c->L / c->S;
@@ -985,10 +993,11 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
         bool done = false;
         if (in_kind == MFH_IN_U16 || in_kind == MFH_IN_U16_SIGNED) {
             SrcU16 s{(const uint16_t *)src, nn, c->n, c->L};
-            done = forward_fast_u16(c, s, dst, in_kind == MFH_IN_U16_SIGNED);
+            done = forward_fast_u16(c, s, dst, in_kind == MFH_IN_U16_SIGNED, r0, rows);
         } else if (in_kind == MFH_IN_F32) {
             SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
-            done = try_fast<4, 16, MFH_MODE_K7, false, SrcF32, LimbsI32<32>>(c, s, dst, 0);
+            done = try_fast<4, 16, MFH_MODE_K7, false, SrcF32, LimbsI32<32>>(c, s, dst, 0, r0,
+                                                                            rows);
         }
         if (done) {
             MFH_HIP(hipGetLastError());
@@ -998,27 +1007,27 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
     switch (in_kind) {
     case MFH_IN_U16: {
         SrcU16 s{(const uint16_t *)src, nn, c->n, c->L};
-        launch_generic<SrcU16>(c, s, dst, grid, LS);
+        launch_generic<SrcU16>(c, s, dst, grid, LS, r0, rows);
         break;
     }
     case MFH_IN_U16_SIGNED: {
         SrcU16Signed s{(const uint16_t *)src, nn, c->n, c->L};
-        launch_generic<SrcU16Signed>(c, s, dst, grid, LS);
+        launch_generic<SrcU16Signed>(c, s, dst, grid, LS, r0, rows);
         break;
     }
     case MFH_IN_I32: {
         SrcI32 s{(const int32_t *)src, nn, c->n, c->L};
-        launch_generic<SrcI32>(c, s, dst, grid, LS);
+        launch_generic<SrcI32>(c, s, dst, grid, LS, r0, rows);
         break;
     }
     case MFH_IN_F32: {
         SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
-        launch_window<SrcF32>(c, s, dst, grid);
+        launch_window<SrcF32>(c, s, dst, grid, r0, rows);
         break;
     }
     case MFH_IN_F64: {
         SrcF64 s{(const double *)src, nn, c->n, c->L, scale_S};
-        launch_window<SrcF64>(c, s, dst, grid);
+        launch_window<SrcF64>(c, s, dst, grid, r0, rows);
         break;
     }
     default:
@@ -1039,7 +1048,8 @@ int mfh_launch_check_i32(mfh_ctx *c, const int32_t *src, int planes)
 
 namespace {
 template <int NB, int K, bool CARRY, int NPASS = 2>
-bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL)
+bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, size_t eb0,
+                         size_t eb1, int r0, int rows)
 {
     constexpr int E = NPASS * (256 / K);
     const int P = 2 * c->L - 1;
@@ -1054,10 +1064,10 @@ bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL)
             return false;
         attr_set = true;
     }
-    const size_t nn = (size_t)c->n * c->n;
-    hipLaunchKernelGGL((k_inverse_fast<NB, K, CARRY, NPASS>), dim3((unsigned)((nn + E - 1) / E)),
-                       dim3(256), lds, c->stream, c->dC5, Cw, out, RL, c->n, c->np, P, c->mode,
-                       mfh_nclasses(c->mode));
+    hipLaunchKernelGGL((k_inverse_fast<NB, K, CARRY, NPASS>),
+                       dim3((unsigned)((eb1 - eb0 + E - 1) / E)), dim3(256), lds, c->stream,
+                       c->dC5, Cw, out, RL, c->n, c->np, P, c->mode, mfh_nclasses(c->mode), eb0,
+                       eb1, r0, rows);
     return true;
 }
 // out != nullptr: fused carry into RL uint16 limbs (Cw is not written).
@@ -1066,22 +1076,28 @@ bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL)
 // carry lookahead this also pays at K = 32, 8 elements per workgroup:
 // inverse + carry 2.15 -> 1.19 ms at n=256, W=8192).
 template <int NB, int K>
-bool try_inverse_fast(mfh_ctx *c, int64_t *Cw, uint16_t *&out, int RL)
+bool try_inverse_fast(mfh_ctx *c, int64_t *Cw, uint16_t *&out, int RL, size_t eb0, size_t eb1,
+                      int r0, int rows)
 {
     if (c->NB != NB || c->K != K) return false;
-    if (out) return try_inverse_fast_as<NB, K, true, 1>(c, Cw, out, RL);
+    if (out) return try_inverse_fast_as<NB, K, true, 1>(c, Cw, out, RL, eb0, eb1, r0, rows);
     out = nullptr;
-    return try_inverse_fast_as<NB, K, false>(c, Cw, out, RL);
+    return try_inverse_fast_as<NB, K, false>(c, Cw, out, RL, eb0, eb1, r0, rows);
 }
 }  // namespace
 
-int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carried)
+int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carried, int r0,
+                       int rows)
 {
     *carried = 0;
-    if (c->use_fast && (try_inverse_fast<32, 16>(c, Cw, out, RL) ||   // W=2048
-                        try_inverse_fast<16, 16>(c, Cw, out, RL) ||   // W=1024
-                        try_inverse_fast<16, 8>(c, Cw, out, RL) ||    // W=512
-                        try_inverse_fast<64, 32>(c, Cw, out, RL))) {  // W=8192
+    if (r0 < 0 || r0 >= c->n || rows < 1 || r0 + rows > c->np) return MFH_E_ARG;
+    const int r1 = r0 + rows < c->n ? r0 + rows : c->n;       // band rows inside the matrix
+    const size_t eb0 = (size_t)r0 * c->n, eb1 = (size_t)r1 * c->n;
+    if (c->use_fast &&
+        (try_inverse_fast<32, 16>(c, Cw, out, RL, eb0, eb1, r0, rows) ||    // W=2048
+         try_inverse_fast<16, 16>(c, Cw, out, RL, eb0, eb1, r0, rows) ||    // W=1024
+         try_inverse_fast<16, 8>(c, Cw, out, RL, eb0, eb1, r0, rows) ||     // W=512
+         try_inverse_fast<64, 32>(c, Cw, out, RL, eb0, eb1, r0, rows))) {   // W=8192
         *carried = out != nullptr;
         MFH_HIP(hipGetLastError());
         return MFH_OK;
@@ -1093,7 +1109,6 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carr
     int threads = epw * c->K;
     if (threads > 1024) { epw = 1024 / c->K; threads = epw * c->K; }
     if (threads < 64) threads = 64;    // keep whole waves; extra threads idle
-    const size_t nn = (size_t)c->n * c->n;
     const size_t lds = (size_t)2 * epw * blk * sizeof(int64_t);
     static bool attr_set = false;
     if (!attr_set) {
@@ -1101,10 +1116,11 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carr
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 131072));
         attr_set = true;
     }
-    dim3 grid((unsigned)((nn + epw - 1) / epw));
+    dim3 grid((unsigned)((eb1 - eb0 + epw - 1) / epw));
     hipLaunchKernelGGL(k_inverse_fold, grid, dim3(threads), lds, c->stream,
                        c->dC5, Cw, c->n, c->np, c->NB, c->K, c->S, c->g,
-                       lg2i(c->NB), 2 * c->L - 1, epw, c->mode, mfh_nclasses(c->mode));
+                       lg2i(c->NB), 2 * c->L - 1, epw, c->mode, mfh_nclasses(c->mode), eb0, eb1,
+                       r0, rows);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }

@@ -70,7 +70,7 @@ def load(path=None):
         "mfh_strerror": ([i], C.c_char_p), "mfh_device_count": ([], i),
         "mfh_device_arch": ([], C.c_char_p),
         "mfh_create": ([C.POINTER(vp), i, i, pl], i), "mfh_destroy": ([vp], None),
-        "mfh_workspace_bytes": ([vp], sz),
+        "mfh_workspace_bytes": ([vp], sz), "mfh_band_rows": ([vp], i),
         "mfh_mm": ([vp, i, vp, vp, vp, i], i), "mfh_conv": ([vp, vp, vp, vp], i),
         "mfh_mm_dev": ([vp, i, vp, vp, vp, i], i), "mfh_conv_dev": ([vp, vp, vp, vp], i),
         "mfh_fpx_mm_dev": ([vp, vp, vp, i, i, vp], i), "mfh_fpx_mm": ([vp, vp, vp, i, i, vp], i),
@@ -218,6 +218,12 @@ class Ctx:
         return out
 
     # device-level helpers
+    def band_rows(self):
+        return self.lib.mfh_band_rows(self.h)
+
+    def workspace_bytes(self):
+        return self.lib.mfh_workspace_bytes(self.h)
+
     def set_timing(self, on=True):
         check(self.lib.mfh_set_timing(self.h, int(on)))
 

@@ -309,12 +309,97 @@ def test_fpx64_random(gpu, orc, lib, n, force, emin, emax):
     assert np.array_equal(dsig, sig) and np.array_equal(dex, ex)
 
 
+# ---- row bands ----------------------------------------------------------------------------
+def banded(monkeypatch, rows):
+    monkeypatch.setenv("MFH_BAND_ROWS", str(rows))
+
+
+def test_row_bands_against_oracle(gpu, orc, monkeypatch):
+    """A in bands of 64 padded rows: the last band holds the last 8 rows."""
+    n, L = 72, 32
+    banded(monkeypatch, 64)
+    A, A32 = signed_limbs(orc, n, L, SEED + 3)
+    B, B32 = signed_limbs(orc, n, L, SEED_B + 3)
+    RL = 2 * L + 1
+    with gpu.Ctx(n, L) as ctx:
+        assert ctx.band_rows() == 64
+        got_u = ctx.mm(A, B, RL)
+        got_s = ctx.mm(A, B, RL, signed=True)
+    assert np.array_equal(got_u, orc.mm_mfft(A, B, n, L, orc.plan(L), RL))
+    want_s = orc.normalize(orc.conv_limbplane(A32, B32, n, L), 2 * L - 1, n, RL)
+    assert np.array_equal(got_s, want_s)
+
+
+@pytest.mark.parametrize("n,L,band", [(200, 128, 64), (100, 128, 64), (130, 32, 64),
+                                      (96, 512, 64), (136, 64, 128), (100, 8, 64),
+                                      (160, 16, 64)])
+def test_row_bands_same_bits(gpu, orc, monkeypatch, n, L, band):
+    """Every ring size, fast (n % 8 == 0) and generic forward transforms,
+    unsigned and signed: banded products equal the one-band products."""
+    print(f"[bands] n={n} L={L} band={band}", flush=True)
+    A = orc.bigmat_rand(n, L, SEED + n)
+    B = orc.bigmat_rand(n, L, SEED_B + n)
+    RL = 2 * L + 1
+    with gpu.Ctx(n, L) as ctx:
+        assert ctx.band_rows() >= n
+        whole = [ctx.mm(A, B, RL), ctx.mm(A, B, RL, signed=True)]
+        full_bytes = ctx.workspace_bytes()
+    banded(monkeypatch, band)
+    with gpu.Ctx(n, L) as ctx:
+        assert ctx.band_rows() == band
+        assert ctx.workspace_bytes() < full_bytes
+        assert np.array_equal(ctx.mm(A, B, RL), whole[0])
+        assert np.array_equal(ctx.mm(A, B, RL, signed=True), whole[1])
+
+
+def test_row_bands_conv_and_floats(gpu, orc, monkeypatch):
+    """Coefficient-plane outputs (conv, then the fp32 and fp64 decodes)."""
+    n, L = 150, 64
+    rng = np.random.default_rng(9)
+    A32 = rng.integers(-65535, 65536, size=L * n * n).astype(np.int32)
+    B32 = rng.integers(-65535, 65536, size=L * n * n).astype(np.int32)
+    X = orc.fp32_rand(n * n, SEED, -30, 30)
+    Y = orc.fp32_rand(n * n, SEED_B, -30, 30)
+    rng = np.random.default_rng(10)
+    Xd = rng.standard_normal(n * n) * np.exp2(rng.integers(-40, 40, n * n))
+    Yd = rng.standard_normal(n * n) * np.exp2(rng.integers(-40, 40, n * n))
+    res = []
+    for band in (0, 64):
+        if band:
+            banded(monkeypatch, band)
+        with gpu.Ctx(n, L) as ctx:
+            assert (ctx.band_rows() == band) if band else ctx.band_rows() >= n
+            res.append([ctx.conv(A32, B32)])
+        with gpu.Ctx(n, 32) as ctx:
+            res[-1].append(ctx.fpx_mm(X, Y, 256, 256).view(np.uint32))
+        with gpu.Ctx(n, 128) as ctx:
+            res[-1].append(ctx.fpx_mm_f64(Xd, Yd, 1024, 1024).view(np.uint64))
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
+
+
+def test_row_bands_generic_kernels(gpu, orc, monkeypatch):
+    """Runtime-plan kernels in bands against the oracle."""
+    monkeypatch.setenv("MFH_GENERIC_KERNELS", "1")
+    banded(monkeypatch, 64)
+    n, L = 80, 32
+    A = orc.bigmat_rand(n, L, SEED)
+    B = orc.bigmat_rand(n, L, SEED_B)
+    RL = 2 * L + 1
+    with gpu.Ctx(n, L) as ctx:
+        assert ctx.band_rows() == 64
+        assert np.array_equal(ctx.mm(A, B, RL), orc.mm_mfft(A, B, n, L, orc.plan(L), RL))
+
+
 # ---- full-size workloads ------------------------------------------------------------------
-def check_large(gpu, orc, lib, n, W, signed):
+def check_large(gpu, orc, lib, n, W, signed, min_bands=1):
     L = W // 16
     RL = 2 * L + 1
     print(f"[large] n={n} W={W} signed={signed}", flush=True)
     with gpu.Ctx(n, L) as ctx:
+        print(f"[large] band rows {ctx.band_rows()}, workspace {ctx.workspace_bytes() / 1e9:.1f} GB",
+              flush=True)
+        assert -(-n // ctx.band_rows()) >= min_bands
         dA, dB, dO = gpu.DevBuf(L * n * n * 2), gpu.DevBuf(L * n * n * 2), gpu.DevBuf(RL * n * n * 2)
         gpu.check(lib.mfh_rand_u16_dev(ctx.h, dA.ptr, n, L, SEED))
         gpu.check(lib.mfh_rand_u16_dev(ctx.h, dB.ptr, n, L, SEED_B))
@@ -368,6 +453,12 @@ def test_n3072_w2048_beyond_the_9_product_bound(gpu, orc, lib):
         for b in (dA, dB, dCw):
             b.free()
     assert rc == -4
+
+
+def test_n4096_w2048_in_row_bands(gpu, orc, lib):
+    """n = 4096 at 2048 bits: the one-band workspace (about 310 GB) exceeds
+    the device, so A goes through in row bands."""
+    check_large(gpu, orc, lib, 4096, 2048, False, min_bands=2)
 
 
 def test_c4_fp32_n2048(gpu, orc):
