@@ -37,17 +37,22 @@
 // Digit modes of the transformed values.
 //  MFH_MODE_B8: three balanced base-2^8 digits d0, d1, d2 in [-128, 127];
 //    9 digit products, accumulated in 5 weight classes m = r+s (2^(8m)).
-//  MFH_MODE_K7: three balanced base-2^7 digits d0, d1, d2 in [-64, 63] plus
-//    the pairwise sums d0+d1, d0+d2, d1+d2 (in [-128, 126], still int8):
+//  MFH_MODE_K7: three balanced base-2^7 digits d0, d1 in [-64, 63] and d2 in
+//    [-64, 64], plus the pairwise sums d0+d1, d0+d2, d1+d2 (in [-128, 127],
+//    still int8; so is every product operand, and |product| <= 2^14):
 //    Karatsuba's 6 products P0 = a0 b0, P1 = a1 b1, P2 = a2 b2,
 //    P3 = (a0+a1)(b0+b1), P4 = (a0+a2)(b0+b2), P5 = (a1+a2)(b1+b2), one
 //    class each, recombined as
 //      c0 = P0, c1 = P3-P0-P1, c2 = P4-P0-P2+P1, c3 = P5-P1-P2, c4 = P2,
 //      C^ = sum_m c_m 2^(7m).
-//    Range: [-64 (1+2^7+2^14), 63 (1+2^7+2^14)] = [-1056832, 1040319].
+//    Range: [-64 (1+2^7+2^14), 63 (1+2^7) + 64 2^14] = [-1056832, 1056703]:
+//    the balanced digits of v are d0 = ((v+64) & 127) - 64,
+//    v1 = (v+64) >> 7, d1 = ((v1+64) & 127) - 64, d2 = (v1+64) >> 7, and over
+//    that range d2 reaches +64 but no further (it is 64 only for
+//    v >= 2^20 - 64).
 #define MFH_MODE_B8 0
 #define MFH_MODE_K7 1
-#define MFH_K7_MAX 1040319LL
+#define MFH_K7_MAX 1056703LL
 #define MFH_PLANES_MAX 6          // digit planes per (point, coefficient)
 #define MFH_CLASSES_MAX 6         // int32 class results per (point, element, t)
 static inline int mfh_planes(int mode) { return mode == MFH_MODE_K7 ? 6 : 3; }
@@ -95,8 +100,12 @@ struct mfh_ctx {
     // workspace
     int mode;             // digit mode of the current product (MFH_MODE_*)
     int recode;           // forward transform recodes limbs to signed form
+    int offset;           // unsigned operands shifted by -2^(W-1) (with recode):
+                          // the inverse adds back 2^(W-1) (r_i + s_j) + 2^(2W-2) n
+    int64_t *dRow;        // offset mode: limb sums of A's rows [L][n] and of B's
+    int64_t *dCol;        //   columns [L][n] (the shifted limbs)
     int k7_ok;            // plan admits MFH_MODE_K7 (workspace sized for it)
-    int b8_ok;            // size admits MFH_MODE_B8's int32 class bound
+    int mode_ok;          // the selected digit setting keeps every bound
     int hb;               // row band height: A's digit planes and the class
                           // results hold hb padded rows at a time
     int8_t *dAh;          // A's digit planes [NB][K][planes][hb][np]
@@ -139,6 +148,9 @@ int mfh_launch_pointwise(mfh_ctx *c, int rows);
 int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carried, int r0,
                        int rows);
 int mfh_launch_carry(mfh_ctx *c, const int64_t *Cw, uint16_t *out, int RL);
+// out[u][r] = sum_k limb_u(r, k) over the rows r of L uint16 planes of n x n,
+// limb L-1 taken as x - 2^15 (offset mode)
+int mfh_launch_offset_sums(const uint16_t *src, int64_t *out, int n, int L, hipStream_t st);
 int mfh_launch_carry_planes(const int64_t *Cw, int P, size_t nn, uint16_t *out,
                             int RL, hipStream_t st);
 // fp32 (is_f64 = 0) or fp64 matrix -> L signed limb planes at scale 2^S
@@ -165,6 +177,9 @@ int mfh_launch_rand_f32(void *dst, size_t count, uint64_t seed, int emin,
 // input kinds used internally for fixed-point float sources
 #define MFH_IN_F32 100
 #define MFH_IN_F64 101
+// unsigned limbs read with 2^(16L-1) subtracted (the top limb as
+// (int16)(x ^ 0x8000)); only the recoding forward transform takes it
+#define MFH_IN_U16_OFFSET 102
 // decode formats: fp32, fp64, 63-bit significand + exponent (long double)
 #define MFH_DEC_F32 0
 #define MFH_DEC_F64 1

@@ -62,23 +62,61 @@ int ensure_staging(mfh_ctx *c, size_t in_bytes, size_t out_bytes)
 }
 
 // Digit mode of a product.  K7 (6 Karatsuba products instead of 9) needs
-// every transformed value inside [-1056832, 1040319]: without recoding
-// |a^| <= (NB/2) 65535; the exact track's forward transform can first
-// recode limbs to [-2^15, 2^15) (top limb <= 2^16), giving
-// |a^| <= (NB/2 + 1) 2^15, for the plans it is specialised for.  conv_mfft
-// must return the convolution of the caller's limbs, so it never recodes.
-bool k7_plain(const mfh_ctx *c) { return (long long)(c->NB / 2) * 65535 <= MFH_K7_MAX; }
-bool k7_recoded(const mfh_ctx *c)
+// every transformed value inside [-1056832, 1056703]; |a^| is at most the
+// sum of NB/2 limb magnitudes (one limb per non-zero block):
+//  * plain limbs: (NB/2) 65535;
+//  * the exact track's forward transform can first recode limbs to
+//    [-2^15, 2^15) with the top limb keeping its carry: up to 2^16 for
+//    unsigned entries, (NB/2 - 1) 2^15 + 2^16; in [-2^15, 2^15] for two's
+//    complement entries, or for unsigned ones shifted by -2^(W-1) (offset
+//    mode, the inverse adds the shift's terms back): (NB/2) 2^15.
+// Recoding runs in the plans the forward transform is specialised for
+// (k7_recode_plan).  conv_mfft must return the convolution of the caller's
+// limbs, so it never recodes.
+//
+// Each setting must also keep the int64 and int32 intermediates exact:
+//  * int64: the inverse sees NB * K * n * |a^| |b^| (NB points of K-term
+//    ring products over n), below 2^62;
+//  * int32 classes: pairs * (np/64) * K * 2^20 (mfh_class_bound_ok), pairs =
+//    1 for K7, 3 for B8.
+bool k7_recode_plan(const mfh_ctx *c)
 {
-    return c->use_fast && c->n % 8 == 0 && c->S == 8 && c->NB == 32 &&
-           (long long)(c->NB / 2 + 1) * 32768 <= MFH_K7_MAX;
+    return c->use_fast && c->n % 8 == 0 &&
+           ((c->S == 8 && c->NB == 32) || (c->S == 16 && c->NB == 64));
 }
-void select_mode(mfh_ctx *c, bool exact_track)
+bool fits(const mfh_ctx *c, long long amax, int pairs)
 {
-    c->recode = 0;
-    if (k7_plain(c)) c->mode = MFH_MODE_K7;
-    else if (exact_track && k7_recoded(c)) { c->mode = MFH_MODE_K7; c->recode = 1; }
-    else c->mode = MFH_MODE_B8;
+    const double bits = log2((double)c->NB) + log2((double)c->K) + log2((double)c->np) +
+                        2.0 * log2((double)amax);
+    return bits < 62.0 && mfh_class_bound_ok(c->K, c->np, pairs);
+}
+// kind: the input of an exact-track product (MFH_IN_U16 or
+// MFH_IN_U16_SIGNED), or -1 for products of the caller's own limbs.  Sets
+// mode / recode / offset to the first setting that fits, in the order
+// recoded K7, plain K7, recoded K7 with symmetric limbs (signed entries, or
+// unsigned ones in offset mode), B8; mode_ok = 0 when none does.
+void select_mode(mfh_ctx *c, int kind)
+{
+    const bool exact = kind == MFH_IN_U16 || kind == MFH_IN_U16_SIGNED;
+    const long long half = c->NB / 2;
+    const long long a_plain = half * 65535, a_rec = (half + 1) * 32768, a_sym = half * 32768;
+    const bool rec = exact && k7_recode_plan(c);
+    struct { bool ok; int mode, recode, offset; } cand[] = {
+        {rec && a_rec <= MFH_K7_MAX && fits(c, a_rec, 1), MFH_MODE_K7, 1, 0},
+        {a_plain <= MFH_K7_MAX && fits(c, a_plain, 1), MFH_MODE_K7, 0, 0},
+        {rec && a_sym <= MFH_K7_MAX && fits(c, a_sym, 1), MFH_MODE_K7, 1, kind == MFH_IN_U16},
+        {a_plain <= MFH_DIGIT_MAX && fits(c, a_plain, 3), MFH_MODE_B8, 0, 0},
+    };
+    c->mode = MFH_MODE_B8;
+    c->recode = c->offset = c->mode_ok = 0;
+    for (const auto &k : cand)
+        if (k.ok) {
+            c->mode = k.mode;
+            c->recode = k.recode;
+            c->offset = k.offset;
+            c->mode_ok = 1;
+            return;
+        }
 }
 
 void mark(mfh_ctx *c, int k)
@@ -100,12 +138,21 @@ int run_conv(mfh_ctx *c, int kind, const void *dA, const void *dB, int64_t *Cw,
              int SA, int SB, uint16_t *out16 = nullptr, int RL = 0, int *carried = nullptr)
 {
     int rc;
-    if (c->mode == MFH_MODE_B8 && !c->b8_ok) return MFH_E_BOUND;
+    if (!c->mode_ok) return MFH_E_BOUND;
     mark(c, 0);
     const int eb = (kind == MFH_IN_U16 || kind == MFH_IN_U16_SIGNED) ? 2
                    : kind == MFH_IN_F64 ? 8 : 4;
     const int planes = (kind == MFH_IN_F32 || kind == MFH_IN_F64) ? 1 : c->L;
     if ((rc = mfh_launch_transpose(dB, c->dBt, planes, c->n, eb, c->stream))) return rc;
+    if (c->offset) {
+        // shifted operands: row sums of A, column sums of B (rows of B^T)
+        if (kind != MFH_IN_U16 || !out16) return MFH_E_UNSUPPORTED;
+        kind = MFH_IN_U16_OFFSET;
+        if ((rc = mfh_launch_offset_sums((const uint16_t *)dA, c->dRow, c->n, c->L, c->stream)) ||
+            (rc = mfh_launch_offset_sums((const uint16_t *)c->dBt, c->dCol, c->n, c->L,
+                                         c->stream)))
+            return rc;
+    }
     if ((rc = mfh_launch_forward(c, kind, c->dBt, c->dBh, SB, 0, c->np))) return rc;
     int fused = 0, b = 0;
     for (int r0 = 0; r0 < c->n; r0 += c->hb, ++b) {
@@ -200,20 +247,19 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     // digit range: |a^| <= (NB/2) * 65535 must fit three balanced int8 digits
     if ((long long)(p->NB / 2) * 65535 > MFH_DIGIT_MAX) return MFH_E_BOUND;
     const int np_ = (n + MFH_KBLK - 1) / MFH_KBLK * MFH_KBLK;
-    // int64: NB (inverse) * K * n * ((NB/2) 65535)^2 < 2^62
-    double bits = log2((double)p->NB) + log2((double)p->K) + log2((double)np_) +
-                  2.0 * log2((double)(p->NB / 2) * 65535.0);
-    if (bits >= 62.0) return MFH_E_BOUND;
-    // int32 classes: the 6-product mode (one product per class) admits 3x
-    // the size of the 9-product mode; a size only the former admits serves
-    // the products that use it (MFH_E_BOUND for the others, at call time)
+    // the int64 and int32 bounds hold for some digit setting of the exact
+    // track (a superset of the others'); a size only some settings admit
+    // serves the products that use them (MFH_E_BOUND for the others, at
+    // call time)
     mfh_ctx shape;
     memset(&shape, 0, sizeof shape);
     shape.n = n; shape.np = np_; shape.L = L; shape.S = p->S; shape.NB = p->NB; shape.K = p->K;
     shape.use_fast = getenv("MFH_GENERIC_KERNELS") ? 0 : 1;
-    const bool k7_ok = k7_plain(&shape) || k7_recoded(&shape);
-    const bool b8_ok = mfh_class_bound_ok(p->K, np_, 3);
-    if (!b8_ok && !(k7_ok && mfh_class_bound_ok(p->K, np_, 1))) return MFH_E_BOUND;
+    select_mode(&shape, MFH_IN_U16);
+    if (!shape.mode_ok) return MFH_E_BOUND;
+    bool k7_ok = shape.mode == MFH_MODE_K7;
+    select_mode(&shape, -1);
+    k7_ok |= shape.mode_ok && shape.mode == MFH_MODE_K7;
     int rc = check_device();
     if (rc) return rc;
 
@@ -222,7 +268,6 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     c->n = n; c->np = np_; c->L = L; c->S = p->S; c->NB = p->NB; c->K = p->K; c->g = p->g;
     c->dev = 0;
     c->use_fast = shape.use_fast;
-    c->b8_ok = b8_ok;
     if (hipSetDevice(0) != hipSuccess || hipStreamCreate(&c->stream) != hipSuccess) {
         delete c;
         return MFH_E_HIP;
@@ -232,7 +277,7 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     c->k7_ok = k7_ok;
     const int planes = c->k7_ok ? MFH_PLANES_MAX : MFH_DIGITS;
     const int classes = c->k7_ok ? MFH_CLASSES_MAX : MFH_CLASSES;
-    select_mode(c, true);
+    select_mode(c, MFH_IN_U16);
     // per padded row of A: its digit planes and its class results
     const size_t digit_row = (size_t)c->NB * c->K * planes * np_;
     const size_t c5_row = (size_t)c->NB * classes * c->K * np_ * sizeof(int32_t);
@@ -249,6 +294,10 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     if (!rc) rc = dalloc(c, (void **)&c->dCw, cw_bytes);
     if (!rc) rc = dalloc(c, &c->dBt, bt_bytes);
     if (!rc) rc = dalloc(c, (void **)&c->dFlag, sizeof(int));
+    if (!rc && k7_recode_plan(c)) {
+        rc = dalloc(c, (void **)&c->dRow, (size_t)L * n * sizeof(int64_t));
+        if (!rc) rc = dalloc(c, (void **)&c->dCol, (size_t)L * n * sizeof(int64_t));
+    }
     if (rc) { mfh_destroy(c); return rc; }
     *out = c;
     return MFH_OK;
@@ -259,7 +308,7 @@ void mfh_destroy(mfh_ctx *c)
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     void *bufs[] = {c->dAh, c->dBh, c->dC5, c->dCw, c->dBt, c->dFlag,
-                    c->dInA, c->dInB, c->dOut};
+                    c->dInA, c->dInB, c->dOut, c->dRow, c->dCol};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     for (int k = 0; k < 5; ++k)
@@ -278,7 +327,7 @@ int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut,
 {
     if (!c || !dA || !dB || !dOut || RL < 1) return MFH_E_ARG;
     if (kind != MFH_IN_U16 && kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
-    select_mode(c, true);
+    select_mode(c, kind);
     int carried = 0;
     int rc = run_conv(c, kind, dA, dB, c->dCw, 0, 0, (uint16_t *)dOut, RL, &carried);
     if (rc) return rc;
@@ -289,9 +338,12 @@ int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut,
 }
 
 // products that return the caller's own limb convolution (conv_mfft, the
-// fixed-point floats) never recode, so they take the 6-product mode only
-// when plain K7 fits, else the 9-product mode and its class bound
-static bool conv_size_ok(const mfh_ctx *c) { return k7_plain(c) || c->b8_ok; }
+// fixed-point floats) never recode: plain K7 or B8, if either fits
+static bool conv_size_ok(mfh_ctx *c)
+{
+    select_mode(c, -1);
+    return c->mode_ok != 0;
+}
 
 int mfh_conv_dev(mfh_ctx *c, const void *dA32, const void *dB32, void *dCw)
 {
@@ -303,7 +355,7 @@ int mfh_conv_dev(mfh_ctx *c, const void *dA32, const void *dB32, void *dCw)
     if ((rc = mfh_launch_check_i32(c, (const int32_t *)dB32, c->L))) return rc;
     if ((rc = read_flag(c, &flag))) return rc;
     if (flag) return MFH_E_RANGE;
-    select_mode(c, false);
+    select_mode(c, -1);
     rc = run_conv(c, MFH_IN_I32, dA32, dB32, (int64_t *)dCw, 0, 0);
     if (rc) return rc;
     c->last_out = 1; c->last_fused = 0;
@@ -317,7 +369,7 @@ int fpx_mm_dev(mfh_ctx *c, int f64, const void *dA, const void *dB, int SA, int 
 {
     if (!c || !dA || !dB || !dC) return MFH_E_ARG;
     if (!conv_size_ok(c)) return MFH_E_BOUND;
-    select_mode(c, false);
+    select_mode(c, -1);
     int rc = run_conv(c, f64 ? MFH_IN_F64 : MFH_IN_F32, dA, dB, c->dCw, SA, SB);
     if (rc) return rc;
     if ((rc = mfh_launch_decode(c, c->dCw, SA + SB, f64 ? MFH_DEC_F64 : MFH_DEC_F32, dC,

@@ -158,8 +158,8 @@ __device__ __forceinline__ long long combine_classes(const int32_t *p, size_t cs
 //  B8: balanced base-2^8 digits, i.e. the low bytes of v, (v + 2^7) >> 8 and
 //      (v + 2^15 + 2^7) >> 16 (each the floor that makes the lower digits
 //      land in [-128, 127]).
-//  K7: balanced base-2^7 digits d0, d1, d2 in [-64, 63] and the sums
-//      d0+d1, d0+d2, d1+d2.
+//  K7: balanced base-2^7 digits d0, d1 in [-64, 63], d2 in [-64, 64] (for
+//      |v| <= 1056703) and the sums d0+d1, d0+d2, d1+d2.
 template <int MODE>
 __device__ __forceinline__ void store_digits(int8_t *p, size_t nnp, int v)
 {
@@ -414,14 +414,15 @@ __device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *
 }
 
 // E elements per workgroup of 256 threads, 256/E threads per element.
+// top: limb L-1 is unsigned (0), int16 (1), or (int16)(x ^ 0x8000), i.e. the
+// entry minus 2^(16L-1) (2, recoding only).
 template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src, int E = 256>
 __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restrict__ out, int np_,
-                                                      int top_signed, int row0, int rows)
+                                                      int top_mode, int row0, int rows)
 {
     constexpr int L = NB * S / 2;
     constexpr int TPE = 256 / E;
     static_assert(E * TPE == 256 && Q % TPE == 0, "threads split evenly over classes");
-    static_assert(!RECODE || TPE == 1, "recoding rewrites the staged limbs in place");
     const size_t nnp = (size_t)rows * np_;           // the band's elements (plane stride)
     const size_t eband = (size_t)row0 * np_;         // its first element in the operand
     const size_t e0 = (size_t)blockIdx.x * E;
@@ -434,30 +435,46 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
         stage_limbs_u16<L, E>(stage, src.p, src.n, src.nn, np_, eband + e0);
         __syncthreads();
         x.base = stage + slot;
-        x.top_signed = top_signed != 0;
+        x.top_signed = top_mode != 0;
         x.recoded = RECODE;
         if constexpr (RECODE) {
             // Signed recoding y_u = x_u + c_u - 2^16 c_(u+1) with
             // c_(u+1) = [x_u + c_u >= 2^15]: the same integer, limbs below
-            // the top in [-2^15, 2^15), the top limb x + c unrecoded.  This
-            // halves the bound on the transformed values.
-            uint32_t *sl = stage + slot;
-            int carry = 0;
+            // the top in [-2^15, 2^15), the top limb (as `top` reads it) + c
+            // unrecoded.  This halves the bound on the transformed values.
+            // One thread per element rewrites the staged limbs; the others
+            // of the element wait for it.
+            __shared__ int top_s[TPE > 1 ? E : 1];
+            if (part == 0) {
+                uint32_t *sl = stage + slot;
+                // padding outside the n x n entries stays 0 (not -2^(16L-1))
+                const size_t eg = eband + e0 + slot;
+                const bool inside = (int)(eg / np_) < src.n && (int)(eg % np_) < src.n;
+                int carry = 0;
 #pragma unroll 8
-            for (int p2 = 0; p2 < L / 2; ++p2) {
-                const uint32_t w = sl[p2 * E];
-                int lo = (int)(w & 0xFFFFu) + carry;
-                carry = lo >= 32768;
-                lo -= carry << 16;
-                int hi = (int)(w >> 16) + carry;
-                if (p2 + 1 < L / 2) {
-                    carry = hi >= 32768;
-                    hi -= carry << 16;
-                } else {
-                    x.top = top_signed ? (int)(short)(w >> 16) + carry : hi;
-                    hi = 0;
+                for (int p2 = 0; p2 < L / 2; ++p2) {
+                    const uint32_t w = sl[p2 * E];
+                    int lo = (int)(w & 0xFFFFu) + carry;
+                    carry = lo >= 32768;
+                    lo -= carry << 16;
+                    int hi = (int)(w >> 16) + carry;
+                    if (p2 + 1 < L / 2) {
+                        carry = hi >= 32768;
+                        hi -= carry << 16;
+                    } else {
+                        const uint32_t t = w >> 16;
+                        x.top = top_mode == 1   ? (int)(short)t + carry
+                                : top_mode == 2 ? (inside ? (int)(short)(t ^ 0x8000u) + carry : 0)
+                                                : hi;
+                        hi = 0;
+                    }
+                    sl[p2 * E] = ((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16);
                 }
-                sl[p2 * E] = ((uint32_t)lo & 0xFFFFu) | ((uint32_t)hi << 16);
+                if constexpr (TPE > 1) top_s[slot] = x.top;
+            }
+            if constexpr (TPE > 1) {
+                __syncthreads();
+                x.top = top_s[slot];
             }
         }
         if (e >= nnp) return;
@@ -569,12 +586,21 @@ __device__ __forceinline__ long long bperm64(long long v, int addr)
 // wave, E <= 64) propagates the carries through the element's 2L-1 planes
 // straight from LDS and writes the RL uint16 output limbs (the semantics of
 // k_carry), saving the int64 round trip through HBM.
+//
+// Offset mode (rowS != nullptr, CARRY only): the operands were A - hJ and
+// B - hJ with h = 2^(16L-1) and J all ones, so
+//     A B = (A-hJ)(B-hJ) + h (r_i + s_j) + h^2 n,
+// r_i / s_j the sums of row i of A-hJ / column j of B-hJ.  With
+// r_i = sum_u rowS[u][i] 2^(16u) (likewise s_j), h r_i adds
+// rowS[u][i] 2^15 to plane L-1+u, and h^2 n adds n 2^14 to plane 2L-1.
 template <int NB, int K, bool CARRY, int NPASS = 2>
 __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict__ C5,
                                                       int64_t *__restrict__ Cw,
                                                       uint16_t *__restrict__ out, int RL,
                                                       int n, int np_, int P, int mode, int ncl,
-                                                      size_t eb0, size_t eb1, int r0, int rows)
+                                                      size_t eb0, size_t eb1, int r0, int rows,
+                                                      const int64_t *__restrict__ rowS,
+                                                      const int64_t *__restrict__ colS)
 {
     constexpr int S = K / 2, g = 2 * K / NB, twoK = 2 * K;
     constexpr int PASS = 256 / K;            // elements per pass
@@ -654,12 +680,26 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
         int len = (RL + SEGS - 1) / SEGS;
         if (len < 4) len = 4;
         const int w0 = sg * len, w1 = min(w0 + len, RL);
+        // plane w of this element, with the offset-mode terms
+        const int Lh = (P + 1) / 2;                    // L
+        const size_t eg = e0 + el < eb1 ? e0 + el : eb0;
+        const int gi = (int)(eg / n), gj = (int)(eg % n);
+        auto plane = [&](int w) -> int64_t {
+            int64_t v = w < P ? cwl[(size_t)w * E + el] : 0;
+            if (rowS) {
+                const int u = w - (Lh - 1);
+                if (u >= 0 && u < Lh)
+                    v += (rowS[(size_t)u * n + gi] + colS[(size_t)u * n + gj]) * 32768;
+                if (w == 2 * Lh - 1) v += (int64_t)n * 16384;
+            }
+            return v;
+        };
         {
             int64_t cc = 0;
             uint64_t low = 0;                          // limbs 0..3 of the run
             bool zero_hi = true, ones_hi = true;       // limbs 4.. all 0 / all 0xFFFF
             for (int w = w0; w < w1; ++w) {
-                const int64_t v = cc + (w < P ? cwl[(size_t)w * E + el] : 0);
+                const int64_t v = cc + plane(w);
                 const uint64_t limb = (uint64_t)(v & 0xFFFF);
                 const int i = w - w0;
                 if (i < 4) low |= limb << (16 * i);
@@ -687,7 +727,7 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
         if (el < ecount) {
             int64_t cc = segin[sg * E + el];
             for (int w = w0; w < w1; ++w) {
-                const int64_t v = cc + (w < P ? cwl[(size_t)w * E + el] : 0);
+                const int64_t v = cc + plane(w);
                 __builtin_nontemporal_store((uint16_t)(v & 0xFFFF), out + (size_t)w * nn + e0 + el);
                 cc = v >> 16;
             }
@@ -713,6 +753,24 @@ __global__ __launch_bounds__(256) void k_carry(const int64_t *__restrict__ Cw,
         out[(size_t)w * nn + e] = (uint16_t)(v & 0xFFFF);
         carry = v >> 16;
     }
+}
+
+// ---- offset-mode limb sums ----------------------------------------------------
+// out[u][r] = sum_k limb_u(r, k) over row r of plane u (n x n, row-major),
+// the top limb (u = L-1) as x - 2^15.  One wave per (u, r); |sum| <= n 2^16.
+__global__ __launch_bounds__(256) void k_offset_sums(const uint16_t *__restrict__ src,
+                                                     int64_t *__restrict__ out, int n, int L)
+{
+    const int lane = threadIdx.x & 63;
+    const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);   // u * n + r
+    if (row >= (size_t)L * n) return;
+    const bool top = (int)(row / n) == L - 1;
+    const uint16_t *p = src + row * n;
+    long long acc = 0;
+    for (int k = lane; k < n; k += 64) acc += top ? (int)p[k] - 32768 : (int)p[k];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+    if (lane == 0) out[row] = acc;
 }
 
 // ---- fixed-point decode (src/fpfixed.c:212-322) ------------------------------
@@ -937,13 +995,14 @@ namespace {
 // compile-time plans: (S, NB) with Q output classes of length NB/Q
 template <int S, int NB, int MODE, bool RECODE, class Src, class Limbs, int E = 256,
           int Q = NB / 4>
-bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_signed, int row0, int rows)
+bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_mode, int row0, int rows)
 {
     if (c->S != S || c->NB != NB || c->mode != MODE || (c->recode != 0) != RECODE) return false;
+    if (top_mode == 2 && !RECODE) return false;
     const size_t nnp = (size_t)rows * c->np;
     hipLaunchKernelGGL((k_forward_fast<S, NB, Q, MODE, RECODE, Limbs, Src, E>),
                        dim3((unsigned)((nnp + E - 1) / E)), dim3(256), 0, c->stream, s, dst,
-                       c->np, top_signed, row0, rows);
+                       c->np, top_mode, row0, rows);
     return true;
 }
 
@@ -954,8 +1013,10 @@ bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, 
     return try_fast<8, 32, K7, true, SrcU16, LimbsLds<128>>(c, s, dst, ts, r0, rows) ||  // W=2048
            try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>>(c, s, dst, ts, r0, rows) ||
            try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>>(c, s, dst, ts, r0, rows) ||  // W=1024
+           try_fast<16, 64, K7, true, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst, ts, r0,
+                                                                        rows) ||    // W=8192
            try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst, ts, r0,
-                                                                         rows) ||   // W=8192
+                                                                         rows) ||
            try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>>(c, s, dst, ts, r0, rows);  // W=512
 }
 }  // namespace
@@ -991,9 +1052,11 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
     const int LS = c->L / c->S;
     if (c->use_fast) {
         bool done = false;
-        if (in_kind == MFH_IN_U16 || in_kind == MFH_IN_U16_SIGNED) {
+        if (in_kind == MFH_IN_U16 || in_kind == MFH_IN_U16_SIGNED ||
+            in_kind == MFH_IN_U16_OFFSET) {
             SrcU16 s{(const uint16_t *)src, nn, c->n, c->L};
-            done = forward_fast_u16(c, s, dst, in_kind == MFH_IN_U16_SIGNED, r0, rows);
+            const int top = in_kind == MFH_IN_U16 ? 0 : in_kind == MFH_IN_U16_SIGNED ? 1 : 2;
+            done = forward_fast_u16(c, s, dst, top, r0, rows);
         } else if (in_kind == MFH_IN_F32) {
             SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
             done = try_fast<4, 16, MFH_MODE_K7, false, SrcF32, LimbsI32<32>>(c, s, dst, 0, r0,
@@ -1030,6 +1093,8 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
         launch_window<SrcF64>(c, s, dst, grid, r0, rows);
         break;
     }
+    case MFH_IN_U16_OFFSET:
+        return MFH_E_UNSUPPORTED;       // recoding kernels only
     default:
         return MFH_E_ARG;
     }
@@ -1067,7 +1132,8 @@ bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, size_t 
     hipLaunchKernelGGL((k_inverse_fast<NB, K, CARRY, NPASS>),
                        dim3((unsigned)((eb1 - eb0 + E - 1) / E)), dim3(256), lds, c->stream,
                        c->dC5, Cw, out, RL, c->n, c->np, P, c->mode, mfh_nclasses(c->mode), eb0,
-                       eb1, r0, rows);
+                       eb1, r0, rows, c->offset ? c->dRow : nullptr,
+                       c->offset ? c->dCol : nullptr);
     return true;
 }
 // out != nullptr: fused carry into RL uint16 limbs (Cw is not written).
@@ -1093,6 +1159,8 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carr
     if (r0 < 0 || r0 >= c->n || rows < 1 || r0 + rows > c->np) return MFH_E_ARG;
     const int r1 = r0 + rows < c->n ? r0 + rows : c->n;       // band rows inside the matrix
     const size_t eb0 = (size_t)r0 * c->n, eb1 = (size_t)r1 * c->n;
+    // offset mode needs the fused carry (it adds the offset terms there)
+    if (c->offset && (!c->use_fast || !out)) return MFH_E_UNSUPPORTED;
     if (c->use_fast &&
         (try_inverse_fast<32, 16>(c, Cw, out, RL, eb0, eb1, r0, rows) ||    // W=2048
          try_inverse_fast<16, 16>(c, Cw, out, RL, eb0, eb1, r0, rows) ||    // W=1024
@@ -1102,6 +1170,7 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carr
         MFH_HIP(hipGetLastError());
         return MFH_OK;
     }
+    if (c->offset) return MFH_E_UNSUPPORTED;
     const int blk = c->NB * c->K;
     int epw = 8192 / blk;              // 2 * epw * blk * 8 bytes <= 128 KiB
     if (epw > 64) epw = 64;
@@ -1121,6 +1190,15 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carr
                        c->dC5, Cw, c->n, c->np, c->NB, c->K, c->S, c->g,
                        lg2i(c->NB), 2 * c->L - 1, epw, c->mode, mfh_nclasses(c->mode), eb0, eb1,
                        r0, rows);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_offset_sums(const uint16_t *src, int64_t *out, int n, int L, hipStream_t st)
+{
+    const size_t rows = (size_t)L * n;
+    hipLaunchKernelGGL(k_offset_sums, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, src,
+                       out, n, L);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }

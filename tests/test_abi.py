@@ -118,11 +118,14 @@ def test_create_checks_arguments_and_bounds(lib):
     assert lib.mfh_create(C.byref(h), 8192, 128, C.byref(p)) == -4
     p64 = M.plan(64)                                   # NB = 16: plain 6-product digits
     assert lib.mfh_create(C.byref(h), 8192, 64, C.byref(p64)) == -4
-    p512 = M.plan(512)                                 # K = 32, 9-product digits only
-    assert lib.mfh_create(C.byref(h), 1408, 512, C.byref(p512)) == -4
+    # K = 32 (8192 bits): the int64 bound NB K n |a^|^2 < 2^62 binds first;
+    # with |a^| <= 2^20 (6-product digits, offset mode) it admits n <= 1984
+    p512 = M.plan(512)
+    assert lib.mfh_create(C.byref(h), 2048, 512, C.byref(p512)) == -4
     if lib.mfh_device_count() == 0:
         assert lib.mfh_create(C.byref(h), 64, 128, C.byref(p)) == -1    # no device
         assert lib.mfh_create(C.byref(h), 3072, 128, C.byref(p)) == -1  # past the bounds
+        assert lib.mfh_create(C.byref(h), 1984, 512, C.byref(p512)) == -1
         assert not h.value
 
 

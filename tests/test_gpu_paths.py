@@ -74,7 +74,7 @@ def test_products_fixture(gpu, orc, case):
     assert np.array_equal(got, np.array(c["out"], dtype=np.uint16))
 
 
-@pytest.mark.parametrize("n,L", [(8, 32), (48, 32), (24, 128), (10, 64), (7, 16)])
+@pytest.mark.parametrize("n,L", [(8, 32), (48, 32), (24, 128), (10, 64), (7, 16), (16, 512)])
 def test_signed_entries(gpu, orc, n, L):
     """Two's complement W-bit entries (top limb int16)."""
     A, A32 = signed_limbs(orc, n, L, SEED + 7)
@@ -105,12 +105,47 @@ def test_short_and_long_outputs(gpu, orc, L, RL):
 
 def test_all_ones_worst_case(gpu, orc):
     """Every limb 0xFFFF: largest transformed values, longest carries."""
-    for n, L in [(64, 128), (16, 64), (32, 32)]:
+    for n, L in [(64, 128), (16, 64), (32, 32), (16, 512)]:
         A = np.full(L * n * n, 0xFFFF, np.uint16)
         RL = 2 * L + 1
         want = orc.mm_limbplane(A, A, n, L, RL)
         with gpu.Ctx(n, L) as ctx:
             assert np.array_equal(ctx.mm(A, A, RL), want), (n, L)
+
+
+@pytest.mark.parametrize("n,L", [(16, 512), (8, 512), (24, 512)])
+def test_offset_mode_extremes(gpu, orc, n, L):
+    """8192-bit unsigned products run shifted by -2^(W-1) (the top limb read
+    as (int16)(x ^ 0x8000)) with the shift's terms added back in the carry;
+    entries at the shift's edges: 0, 2^(W-1) - 1, 2^(W-1), 2^W - 1, and
+    random, mixed per entry.  Checked against the schoolbook oracle, and the
+    two's complement products of the same limbs too."""
+    rng = np.random.default_rng(n * L + 1)
+    nn = n * n
+
+    def pick(seed):
+        A = orc.bigmat_rand(n, L, seed).reshape(L, nn)
+        kind = rng.integers(0, 5, nn)
+        A[:, kind == 0] = 0
+        A[:, kind == 1] = 0xFFFF
+        A[:, kind == 1] = 0xFFFF
+        A[:L - 1, kind == 2] = 0xFFFF                     # 2^(W-1) - 1
+        A[L - 1, kind == 2] = 0x7FFF
+        A[:L - 1, kind == 3] = 0                          # 2^(W-1)
+        A[L - 1, kind == 3] = 0x8000
+        return A.reshape(-1).copy()
+
+    A, B = pick(SEED), pick(SEED_B)
+    RL = 2 * L + 1
+    with gpu.Ctx(n, L) as ctx:
+        got = ctx.mm(A, B, RL)
+        got_s = ctx.mm(A, B, RL, signed=True)
+    assert np.array_equal(got, orc.mm_limbplane(A, B, n, L, RL))
+    A32, B32 = A.astype(np.int32), B.astype(np.int32)
+    A32[(L - 1) * nn:] = A[(L - 1) * nn:].view(np.int16)
+    B32[(L - 1) * nn:] = B[(L - 1) * nn:].view(np.int16)
+    want_s = orc.normalize(orc.conv_limbplane(A32, B32, n, L), 2 * L - 1, n, RL)
+    assert np.array_equal(got_s, want_s)
 
 
 def test_carry_runs_of_ones_and_zeros(gpu):
@@ -441,11 +476,18 @@ def test_c5_n4096_w512_signed(gpu, orc, lib):
 
 
 def test_n3072_w2048_beyond_the_9_product_bound(gpu, orc, lib):
-    """n = 3072 at 2048 bits: the exact track's 6-product digits keep the
-    int32 classes in range (the 9-product mode would not), so mm_mfft works;
-    conv_mfft, which must use 9-product digits at this plan, is refused."""
+    """n = 3072 at 2048 bits: 6-product digits keep the int32 classes in
+    range (the 9-product mode would not)."""
     check_large(gpu, orc, lib, 3072, 2048, False)
-    n, L = 3072, 128
+
+
+def test_w8192_conv_refused_beyond_the_9_product_bound(gpu, lib):
+    """n = 1408 at 8192 bits: the exact track (6-product digits in offset
+    mode, |a^| <= 2^20) admits it; conv_mfft, whose plain limbs need
+    9-product digits here (|a^| up to 2^21), would pass the int64 bound
+    NB K n |a^|^2 < 2^62 only up to n = 512 and is refused at call time,
+    before any kernel runs."""
+    n, L = 1408, 512
     with gpu.Ctx(n, L) as ctx:
         dA, dB = gpu.DevBuf(L * n * n * 4), gpu.DevBuf(L * n * n * 4)
         dCw = gpu.DevBuf((2 * L - 1) * n * n * 8)
