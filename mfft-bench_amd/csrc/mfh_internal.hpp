@@ -74,6 +74,21 @@ __host__ __device__ inline size_t mfh_c5_index(int j, int i, int jj, int t, int 
     const size_t row = ((size_t)j * rows + i) * ncl;           // class 0 of (j, i)
     return ((row * (np_ / 16) + jj / 16) * (K / 4) + t / 4) * 64 + (jj & 15) * 4 + (t & 3);
 }
+// Layout of a digit plane (rows x np int8, rows a multiple of 16, np of
+// 64): 16 x 64 tiles of 1 KB, row-major inside a tile, tiles row-major, so
+// that one MFMA operand fragment (16 rows x 64 k) is one contiguous 1 KB.
+__host__ __device__ inline size_t mfh_tile_off(int i, int k, int np_)
+{
+    return ((size_t)(i >> 4) * (np_ >> 6) + (k >> 6)) * 1024 + (i & 15) * 64 + (k & 63);
+}
+// inverse of mfh_tile_off: the element at offset e of a tiled plane
+__host__ __device__ inline void mfh_tile_ik(size_t e, int np_, int &i, int &k)
+{
+    const size_t t = e >> 10;
+    const int tpr = np_ >> 6;                      // tiles per tile row
+    i = (int)(t / tpr) * 16 + (int)((e >> 6) & 15);
+    k = (int)(t % tpr) * 64 + (int)(e & 63);
+}
 __host__ __device__ inline size_t mfh_c5_class_stride(int np_, int K)
 {
     return (size_t)K * np_;

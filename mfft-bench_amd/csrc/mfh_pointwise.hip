@@ -26,9 +26,10 @@
 // suffices; the orientation of the accumulator (+(P-N) or -(P-N)) is known
 // from the direction of the last round and applied at the flush.
 //
-// Operands in HBM: digit plane (j, c, r) is an int8 matrix, row-major with
-// the reduction index k contiguous (A as A[i][k], B stored transposed as
-// B^T[j'][k]); B's planes hold all np rows, A's the `rows` rows of the
+// Operands in HBM: digit plane (j, c, r) is an int8 matrix with the
+// reduction index k along rows (A as A[i][k], B stored transposed as
+// B^T[j'][k]), in 16 x 64 tiles (mfh_tile_off): one operand fragment is 1 KB
+// contiguous.  B's planes hold all np rows, A's the `rows` rows of the
 // current row band.  Each round stages, for all K ring
 // coefficients, a (16*WBI) x 64 tile of A and a (16*WBJ) x 64 tile of B^T
 // into LDS in MFMA operand order (lane l of a 16x64 fragment = row l%16,
@@ -360,12 +361,14 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     // this wave's fragments f = wave + W*i:
     //   A: coefficient f / WBI, row block f % WBI
     //   B: coefficient f / WBJ, column block f % WBJ
+    // planes in 16 x 64 tiles (mfh_tile_off): a fragment is 1 KB contiguous,
+    // lane l's 16 bytes at row l % 16, k 16 (l / 16) of the tile
     const int8_t *a_blk = Aj + (size_t)(wave / WBI) * PL * planeA +
-                          (size_t)(i0 + (wave % WBI) * 16) * np_ +
-                          (lane & 15) * np_ + (lane >> 4) * 16;
+                          mfh_tile_off(i0 + (wave % WBI) * 16, 0, np_) + (lane & 15) * 64 +
+                          (lane >> 4) * 16;
     const int8_t *b_blk = Bj + (size_t)(wave / WBJ) * PL * plane +
-                          (size_t)(j0 + (wave % WBJ) * 16) * np_ +
-                          (lane & 15) * np_ + (lane >> 4) * 16;
+                          mfh_tile_off(j0 + (wave % WBJ) * 16, 0, np_) + (lane & 15) * 64 +
+                          (lane >> 4) * 16;
     const size_t da = (size_t)(W / WBI) * PL * planeA;
     const size_t db = (size_t)(W / WBJ) * PL * plane;
     v4i *wa = lds + wave * 64 + lane;                     // this lane's A slot of fragment f=wave
@@ -381,8 +384,8 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
     // copy fills (DMA mode): the round's A or B tiles straight into LDS
     auto srcs = [&](RoundPos q, const int8_t *&a0, const int8_t *&b0) {
         const int s = MODE == MFH_MODE_K7 ? q.r : q.m - q.r;
-        a0 = a_blk + (size_t)q.r * planeA + q.kb * MFH_KBLK;
-        b0 = b_blk + (size_t)s * plane + q.kb * MFH_KBLK;
+        a0 = a_blk + (size_t)q.r * planeA + q.kb * 1024;        // next tile along k
+        b0 = b_blk + (size_t)s * plane + q.kb * 1024;
     };
     auto dma_a = [&](RoundPos q) {
         const int8_t *a0, *b0;
@@ -406,8 +409,8 @@ k_pointwise(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
         const int s = MODE == MFH_MODE_K7 ? r : q.m - r;
 #pragma unroll
         for (int sb = 0; sb < KB; ++sb) {
-            const int8_t *a0 = a_blk + (size_t)r * planeA + (kb * KB + sb) * MFH_KBLK;
-            const int8_t *b0 = b_blk + (size_t)s * plane + (kb * KB + sb) * MFH_KBLK;
+            const int8_t *a0 = a_blk + (size_t)r * planeA + (kb * KB + sb) * 1024;
+            const int8_t *b0 = b_blk + (size_t)s * plane + (kb * KB + sb) * 1024;
 #pragma unroll
             for (int i = 0; i < NA; ++i) R[sb * NF + i] = *(const v4i *)(a0 + i * da);
 #pragma unroll

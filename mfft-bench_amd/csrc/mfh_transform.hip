@@ -185,9 +185,9 @@ __device__ __forceinline__ void store_digits(int8_t *p, size_t nnp, int v)
 // One thread per padded element (i, k) of a band of `rows` padded rows from
 // row0 of an np x np operand; it writes the digit planes of every (point j,
 // coefficient c).  Elements outside the n x n input are zero.  Output plane
-// (j, c, r) holds digit r of X[j][c] as a rows x np row-major int8 matrix
-// (the whole operand when row0 = 0, rows = np; the other forward kernels
-// take the same band).
+// (j, c, r) holds digit r of X[j][c] as a rows x np int8 matrix in 16 x 64
+// tiles (mfh_tile_off; the whole operand when row0 = 0, rows = np; the other
+// forward kernels take the same band and layout).
 template <class Src, int MODE>
 __global__ __launch_bounds__(256) void k_forward_generic(
     Src src, int8_t *__restrict__ out, int np_, int LS, int S, int NB, int K,
@@ -198,6 +198,7 @@ __global__ __launch_bounds__(256) void k_forward_generic(
     if (e >= nnp) return;
     const int i = row0 + (int)(e / np_), k = (int)(e % np_);
     const bool valid = i < src.n && k < src.n;
+    const size_t toff = mfh_tile_off(i - row0, k, np_);
     const int twoK = 2 * K;
     for (int j = 0; j < NB; ++j) {
         for (int c = 0; c < K; ++c) {
@@ -212,7 +213,7 @@ __global__ __launch_bounds__(256) void k_forward_generic(
                 }
             }
             constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
-            store_digits<MODE>(out + ((size_t)(j * K + c) * PL) * nnp + e, nnp, acc);
+            store_digits<MODE>(out + ((size_t)(j * K + c) * PL) * nnp + toff, nnp, acc);
         }
     }
 }
@@ -233,6 +234,7 @@ __global__ __launch_bounds__(256) void k_forward_window(Src src, int8_t *__restr
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= nnp) return;
     const int i = row0 + (int)(e / np_), k = (int)(e % np_);
+    const size_t toff = mfh_tile_off(i - row0, k, np_);
     int lo = src.L, r[NW];
     if (i < src.n && k < src.n) src.window(i, k, lo, r);
     int b[NW], s[NW];
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(256) void k_forward_window(Src src, int8_t *__restr
 #pragma unroll
             for (int t = 0; t < NW; ++t) acc += p[t] == c ? r[t] : p[t] == c + K ? -r[t] : 0;
             constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
-            store_digits<MODE>(out + ((size_t)(j * K + c) * PL) * nnp + e, nnp, acc);
+            store_digits<MODE>(out + ((size_t)(j * K + c) * PL) * nnp + toff, nnp, acc);
         }
     }
 }
@@ -296,6 +298,8 @@ struct LimbsLds {
     }
 };
 
+// e0: the first element in tile order (mfh_tile_ik); 8 consecutive
+// elements in tile order are 8 consecutive columns of one row
 template <int L, int E>
 __device__ __forceinline__ void stage_limbs_u16(uint32_t *lds, const uint16_t *src, int n,
                                                 size_t nn, int np_, size_t e0)
@@ -304,7 +308,8 @@ __device__ __forceinline__ void stage_limbs_u16(uint32_t *lds, const uint16_t *s
     for (int t = threadIdx.x; t < NP2 * R8; t += 256) {
         const int p = t / R8, g8 = t % R8;
         const size_t e = e0 + 8 * g8;
-        const int i = (int)(e / np_), k = (int)(e % np_);
+        int i, k;
+        mfh_tile_ik(e, np_, i, k);
         uint4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
         if (i < n && k < n) {
             lo = *(const uint4 *)(src + (size_t)(2 * p) * nn + (size_t)i * n + k);
@@ -414,6 +419,10 @@ __device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *
 }
 
 // E elements per workgroup of 256 threads, 256/E threads per element.
+// Elements are enumerated in the digit planes' tile order (element e of the
+// band is at offset e of every plane), so the 256 consecutive elements of a
+// workgroup are 4 whole rows of one 16 x 64 tile: 256 contiguous bytes of
+// each plane.
 // top: limb L-1 is unsigned (0), int16 (1), or (int16)(x ^ 0x8000), i.e. the
 // entry minus 2^(16L-1) (2, recoding only).
 template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src, int E = 256>
@@ -448,8 +457,9 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
             if (part == 0) {
                 uint32_t *sl = stage + slot;
                 // padding outside the n x n entries stays 0 (not -2^(16L-1))
-                const size_t eg = eband + e0 + slot;
-                const bool inside = (int)(eg / np_) < src.n && (int)(eg % np_) < src.n;
+                int gi, gk;
+                mfh_tile_ik(eband + e0 + slot, np_, gi, gk);
+                const bool inside = gi < src.n && gk < src.n;
                 int carry = 0;
 #pragma unroll 8
                 for (int p2 = 0; p2 < L / 2; ++p2) {
@@ -480,7 +490,9 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
         if (e >= nnp) return;
     } else {
         if (e >= nnp) return;
-        const int i = row0 + (int)(e / np_), k = (int)(e % np_);
+        int i, k;
+        mfh_tile_ik(e, np_, i, k);
+        i += row0;
         const bool valid = i < src.n && k < src.n;
         load_limbs<L>(x, src, i, k, valid);
     }
