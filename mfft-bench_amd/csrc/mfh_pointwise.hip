@@ -593,10 +593,12 @@ int mfh_launch_pointwise(mfh_ctx *c, int rows)
     // one workgroup per CU (64 x 64 tiles, 16 waves at 4 per SIMD, 116
     // VGPRs; 64 x 32 tiles, 8 waves at 2 per SIMD, 214 VGPRs): measured
     // 11-13 % (K = 8) and 5 % (K = 16) faster than two workgroups per CU
-    // with half the tile.  For K = 16 the barrier and the copies come after
-    // the round's third step of MFMAs, so the MFMAs start as soon as this
-    // wave's fragments are in (another 4 %; for K = 8 it is slower).
-    case 8:  return launch_cfg<PwCfg<8, 8, 4, 4, 1, 4, true, 1>>(c, rows);
+    // with half the tile.  The barrier and the copies come after the
+    // round's third (K = 16) or second (K = 8) step of MFMAs, so the MFMAs
+    // start as soon as this wave's fragments are in (4 % for K = 16; with
+    // the tiled planes 6.6 % for K = 8 at n = 4096, against the barrier
+    // before the first step).
+    case 8:  return launch_cfg<PwCfg<8, 8, 4, 4, 1, 4, true, 3>>(c, rows);
     case 16: return launch_cfg<PwCfg<16, 16, 4, 2, 1, 2, true, 4>>(c, rows);
     // K = 32: the same with one 4-wave workgroup per CU at one wave per
     // SIMD (fragments and accumulators need 256 VGPRs + 214 AGPRs; 6 %
