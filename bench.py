@@ -235,6 +235,12 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--n", type=int, default=0,
+                    help="with --bits: an exact-track workload of this size instead of --config "
+                         "(the reference bench's --n / --bits, src/main.c:333-366)")
+    ap.add_argument("--bits", type=int, default=0, help="entry width W (a power of two >= 32)")
+    ap.add_argument("--signed", action="store_true",
+                    help="with --n/--bits: two's complement entries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
@@ -274,6 +280,13 @@ def main():
         dst.free()
         return
 
+    if args.n or args.bits:
+        if not (args.n > 0 and args.bits >= 32 and args.bits & (args.bits - 1) == 0):
+            log("bench.py: --n N --bits W needs N >= 1 and W a power of two >= 32")
+            sys.exit(2)
+        CONFIGS["custom"] = (args.n, args.bits, "signed" if args.signed else "unsigned")
+        args.config = "custom"
+
     if args.table or args.csv:
         method_table(args)
         return
@@ -305,7 +318,8 @@ def main():
         else:
             M.check(lib.mfh_mm_dev(ctx.h, kind, dA.ptr, dB.ptr, dO.ptr, RL), "mfh_mm_dev")
 
-    log(f"[bench] {args.config}: n={n} W={W} L={L} plan={p} warmup={args.warmup} steps={args.steps}")
+    log(f"[bench] {args.config}: n={n} W={W} L={L} plan={p} warmup={args.warmup} steps={args.steps}"
+        f" row band {ctx.band_rows()} of {-(-n // 64) * 64} padded rows")
     for _ in range(args.warmup):
         step()
     ctx.sync()

@@ -1029,7 +1029,9 @@ bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, 
                                                                         rows) ||    // W=8192
            try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst, ts, r0,
                                                                          rows) ||
-           try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>>(c, s, dst, ts, r0, rows);  // W=512
+           try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>>(c, s, dst, ts, r0, rows) ||  // W=512
+           try_fast<16, 32, K7, false, SrcU16, LimbsLds<256, 64>, 64, 16>(c, s, dst, ts, r0,
+                                                                         rows);    // W=4096
 }
 }  // namespace
 
@@ -1177,6 +1179,7 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carr
         (try_inverse_fast<32, 16>(c, Cw, out, RL, eb0, eb1, r0, rows) ||    // W=2048
          try_inverse_fast<16, 16>(c, Cw, out, RL, eb0, eb1, r0, rows) ||    // W=1024
          try_inverse_fast<16, 8>(c, Cw, out, RL, eb0, eb1, r0, rows) ||     // W=512
+         try_inverse_fast<32, 32>(c, Cw, out, RL, eb0, eb1, r0, rows) ||    // W=4096
          try_inverse_fast<64, 32>(c, Cw, out, RL, eb0, eb1, r0, rows))) {   // W=8192
         *carried = out != nullptr;
         MFH_HIP(hipGetLastError());

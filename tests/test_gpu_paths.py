@@ -89,8 +89,8 @@ def test_signed_entries(gpu, orc, n, L):
 
 
 @pytest.mark.parametrize("L,RL", [(64, 1), (64, 5), (64, 64), (64, 129), (32, 3), (32, 70),
-                                  (128, 2), (128, 100), (128, 262), (512, 1), (512, 37),
-                                  (512, 1030)])
+                                  (128, 2), (128, 100), (128, 262), (256, 3), (256, 300),
+                                  (256, 515), (512, 1), (512, 37), (512, 1030)])
 def test_short_and_long_outputs(gpu, orc, L, RL):
     """RL below 2L+1 truncates mod 2^(16 RL), above it zero-extends
     (src/bigmat.c:48-60); every ring size, so every fused-carry layout."""
@@ -105,7 +105,7 @@ def test_short_and_long_outputs(gpu, orc, L, RL):
 
 def test_all_ones_worst_case(gpu, orc):
     """Every limb 0xFFFF: largest transformed values, longest carries."""
-    for n, L in [(64, 128), (16, 64), (32, 32), (16, 512)]:
+    for n, L in [(64, 128), (16, 64), (32, 32), (16, 512), (16, 256)]:
         A = np.full(L * n * n, 0xFFFF, np.uint16)
         RL = 2 * L + 1
         want = orc.mm_limbplane(A, A, n, L, RL)
@@ -367,7 +367,7 @@ def test_row_bands_against_oracle(gpu, orc, monkeypatch):
 
 @pytest.mark.parametrize("n,L,band", [(200, 128, 64), (100, 128, 64), (130, 32, 64),
                                       (96, 512, 64), (136, 64, 128), (100, 8, 64),
-                                      (160, 16, 64)])
+                                      (160, 16, 64), (136, 256, 64)])
 def test_row_bands_same_bits(gpu, orc, monkeypatch, n, L, band):
     """Every ring size, fast (n % 8 == 0) and generic forward transforms,
     unsigned and signed: banded products equal the one-band products."""
@@ -501,6 +501,10 @@ def test_n4096_w2048_in_row_bands(gpu, orc, lib):
     """n = 4096 at 2048 bits: the one-band workspace (about 310 GB) exceeds
     the device, so A goes through in row bands."""
     check_large(gpu, orc, lib, 4096, 2048, False, min_bands=2)
+
+
+def test_n1024_w4096(gpu, orc, lib):
+    check_large(gpu, orc, lib, 1024, 4096, False)
 
 
 def test_c4_fp32_n2048(gpu, orc):
