@@ -256,7 +256,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, "
-              f"WORLD_SIZE={world}); the multi-GPU sharding is described in DESIGN.md",
+              f"WORLD_SIZE={world}); products shard over GPUs by output tiles with no "
+              f"exchange step, which this library does not implement",
               file=sys.stderr)
         sys.exit(2)
 
