@@ -255,7 +255,7 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, "
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE={world}); products shard over GPUs by output tiles with no "
               f"exchange step, which this library does not implement",
               file=sys.stderr)
