@@ -6,6 +6,7 @@ import ctypes as C
 import os
 import re
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -232,3 +233,22 @@ def test_profile_globals_and_leaf_call_counter(lib):
     lib.mfft_profile_reset()
     assert (prof.pack, prof.transform, prof.pointwise, prof.n_fft) == (0.0, 0.0, 0.0, 0)
     assert C.sizeof(M.ProfileT) == 56
+
+
+# ---- bench.py's argument contract (host logic, no GPU call) -------------------
+def _bench(*args):
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    return subprocess.run([sys.executable, os.path.join(root, "bench.py"), *args],
+                          capture_output=True, text=True, timeout=120)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = _bench("--gpus", "2")
+    assert r.returncode == 2 and "one GPU only" in r.stderr
+
+
+@pytest.mark.parametrize("args", [("--n", "100", "--bits", "48"), ("--n", "0", "--bits", "2048"),
+                                  ("--n", "64", "--bits", "16")])
+def test_bench_rejects_bad_sizes(args):
+    r = _bench(*args)
+    assert r.returncode == 2 and "power of two" in r.stderr
