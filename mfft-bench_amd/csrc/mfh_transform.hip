@@ -395,6 +395,7 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
 #pragma unroll
         for (int c = 0; c < K; ++c)
             store_digits<MODE>(o + (size_t)((j * K + c) * PL) * nnp, nnp, z[pos][c]);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -404,7 +405,12 @@ template <int S, int NB, int Q, int MODE, int TPE, int PART, class Limbs, int...
 __device__ __forceinline__ void forward_part(const Limbs &x, int8_t *o, size_t nnp,
                                              std::integer_sequence<int, is...>)
 {
-    (forward_class<S, NB, Q, PART + TPE * is, MODE, Limbs>(x, o, nnp), ...);
+    // scheduling barriers between classes (and after each point's stores,
+    // in forward_class): left free, the scheduler interleaves classes and
+    // the S = 16 kernels need 256+ registers (140 with the barriers)
+    ((forward_class<S, NB, Q, PART + TPE * is, MODE, Limbs>(x, o, nnp),
+      __builtin_amdgcn_sched_barrier(0)),
+     ...);
 }
 template <int S, int NB, int Q, int MODE, int TPE, class Limbs, int PART = 0>
 __device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *o, size_t nnp)
