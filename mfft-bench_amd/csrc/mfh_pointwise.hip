@@ -62,14 +62,22 @@ constexpr int pmod(int a, int m) { return ((a % m) + m) % m; }
 // are copied in while this round's MFMAs run from registers.  BREG = 1: the
 // barrier that frees the buffer and the copies come before the first MFMA;
 // BREG = s + 2: after step s of the round's MFMAs.
+// SHELL: (BREG >= 2 only) lookahead D > 0 selects the shell schedule of
+// pw_round: fragment pairs are read D pairs ahead of the MFMAs that need
+// them, and BREG - 2 counts shells instead of steps.
 template <int K_, int T_, int WBI_, int WBJ_, int KB_ = 1, int WPE_ = 2, bool DMA_ = false,
-          int BREG_ = 0>
+          int BREG_ = 0, int SHELL_ = 0>
 struct PwCfg {
     static constexpr int K = K_, T = T_, WBI = WBI_, WBJ = WBJ_, KB = KB_, WPE = WPE_;
     static constexpr bool DMA = DMA_;
     static constexpr int BREG = BREG_;
+    static constexpr int SHELL = SHELL_;
     static_assert(!DMA || (KB == 1 && T == K), "copy fills: one k block, whole-ring waves");
     static_assert(!BREG || DMA, "B fragments in registers: copy fills only");
+    // every LDS read of the round is issued before the barrier that frees
+    // the buffer: the last pair is read at shell K-1-D
+    static_assert(!SHELL || (BREG >= 2 && BREG - 2 >= K - 1 - SHELL && BREG - 2 < K),
+                  "shell schedule: the barrier follows the round's last LDS read");
     static_assert(KB == 1 || KB == 2, "one or two k blocks per fill");
     static constexpr int G = K / T;                 // t-groups per block
     static constexpr int WAVES = WBI * WBJ * G;
@@ -97,6 +105,71 @@ __device__ __forceinline__ void pw_round(v4i (&acc)[Cfg::T], const v4i *__restri
 {
     constexpr int K = Cfg::K, T = Cfg::T;
     constexpr int SA = Cfg::WBI * 64, SB = Cfg::WBJ * 64;
+    if constexpr (T == K && Cfg::SHELL > 0) {
+        // Shell schedule.  The K x K products (c1, c2) are issued in shells:
+        // ascending rounds by m = max(c1, c2) = 0, 1, .., K-1, descending
+        // rounds by m = min(c1, c2) = K-1, .., 0.  Shell m needs only the
+        // fragment pairs (A_c, B_c) up to (down to) c = m, so a wave starts
+        // its MFMAs once its first pair is in and reads the others D pairs
+        // ahead (D*2 reads in flight: the LDS counter tracks at most 15).
+        // Signs: ASC, the positive terms of acc[t] (c1 + c2 = t) all have
+        // max <= t and its negative ones (c1 + c2 = t + K) max >=
+        // ceil((t + K) / 2) >= t + 2 for t <= K-3, so acc[t] is flipped at
+        // the start of shell min(t + 2, K - 1), and acc[K-1] (no negative
+        // terms) after the round.  DESC: the negative terms of acc[t] have
+        // min >= t + 1 and its positive ones min <= t / 2, so acc[t] is
+        // flipped at the start of shell max(t - 1, 0).  One flip per
+        // accumulator per round, as in the step schedule, each at least
+        // one shell away from the MFMAs around it.
+        constexpr int D = Cfg::SHELL;
+        v4i af[K], bf[K];
+#pragma unroll
+        for (int s = 0; s < D && s < K; ++s) {
+            const int c = ASC ? s : K - 1 - s;
+            af[c] = la[c * SA];
+            bf[c] = lb[c * SB];
+        }
+#pragma unroll
+        for (int sh = 0; sh < K; ++sh) {
+            const int m = ASC ? sh : K - 1 - sh;
+            if (sh + D < K) {
+                const int c = ASC ? sh + D : K - 1 - sh - D;
+                af[c] = la[c * SA];
+                bf[c] = lb[c * SB];
+            }
+            if (ASC) {
+                if (m >= 2) acc[m - 2] = -acc[m - 2];
+                if (m == K - 1) acc[K - 2] = -acc[K - 2];
+#pragma unroll
+                for (int c2 = 0; c2 <= m; ++c2) {
+                    const int t = (m + c2) % K;
+                    acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[m], bf[c2], acc[t], 0, 0, 0);
+                }
+#pragma unroll
+                for (int c1 = 0; c1 < m; ++c1) {
+                    const int t = (c1 + m) % K;
+                    acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[c1], bf[m], acc[t], 0, 0, 0);
+                }
+            } else {
+                if (m + 1 < K) acc[m + 1] = -acc[m + 1];
+                if (m == 0) acc[0] = -acc[0];
+#pragma unroll
+                for (int c2 = K - 1; c2 >= m; --c2) {
+                    const int t = (m + c2) % K;
+                    acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[m], bf[c2], acc[t], 0, 0, 0);
+                }
+#pragma unroll
+                for (int c1 = K - 1; c1 > m; --c1) {
+                    const int t = (c1 + m) % K;
+                    acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[c1], bf[m], acc[t], 0, 0, 0);
+                }
+            }
+            issue(sh);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (ASC) acc[K - 1] = -acc[K - 1];
+        return;
+    }
     if constexpr (T == K) {
         // every A fragment is live at every step: hold all K of them.
         // Step st uses B fragment c2 (ascending or descending).  The
@@ -318,10 +391,11 @@ __device__ __forceinline__ void class_pairs(int m, int &rlo, int &npairs)
 // MFMAs read the LDS buffer, the next round's fragments stream from global
 // memory into VGPRs; after the round they are written to LDS (one buffer
 // per workgroup).  With Cfg::DMA the buffer is refilled by buffer-to-LDS
-// copies: with Cfg::BREG every wave first reads all its A and B fragments of
-// the round into registers, and once every wave has (a barrier, before the
-// first MFMA or after an early step) both tiles of the next round are
-// copied in while the MFMAs run; without it the A tile is copied during the
+// copies: with Cfg::BREG every wave reads all its A and B fragments of the
+// round into registers (up front, or with Cfg::SHELL a few pairs ahead of
+// the MFMAs that use them), and once every wave has (a barrier, before the
+// first MFMA or after an early step or shell) both tiles of the next round
+// are copied in while the MFMAs run; without it the A tile is copied during the
 // round and the B tile after it, while the other workgroups on the CU keep
 // the MFMA units busy.
 //
@@ -591,19 +665,23 @@ int mfh_launch_pointwise(mfh_ctx *c, int rows)
     case 4:  return launch_cfg<PwCfg<4, 4, 2, 2>>(c, rows);
     // K = 8 and K = 16: copy fills with the B fragments held in registers,
     // one workgroup per CU (64 x 64 tiles, 16 waves at 4 per SIMD, 116
-    // VGPRs; 64 x 32 tiles, 8 waves at 2 per SIMD, 214 VGPRs): measured
+    // VGPRs; 64 x 32 tiles, 8 waves at 2 per SIMD, 232 VGPRs): measured
     // 11-13 % (K = 8) and 5 % (K = 16) faster than two workgroups per CU
-    // with half the tile.  The barrier and the copies come after the
-    // round's third (K = 16) or second (K = 8) step of MFMAs, so the MFMAs
-    // start as soon as this wave's fragments are in (4 % for K = 16; with
-    // the tiled planes 6.6 % for K = 8 at n = 4096, against the barrier
-    // before the first step).
-    case 8:  return launch_cfg<PwCfg<8, 8, 4, 4, 1, 4, true, 3>>(c, rows);
-    case 16: return launch_cfg<PwCfg<16, 16, 4, 2, 1, 2, true, 4>>(c, rows);
+    // with half the tile.  Shell schedule with fragment pairs read 4 (K = 8)
+    // or 7 (K = 16) pairs ahead; the barrier and the copies come after
+    // shell 3 (K = 8) or 11 (K = 16), the earliest points at which every
+    // read of the round has been issued.  Against the step schedule
+    // (all A fragments before the first MFMA, barrier after step 1 or 2):
+    // pointwise 1.2 % (K = 8, n = 4096) and 1.5-2 % (K = 16, n = 1024)
+    // faster; barriers one to three shells later were 2-11 % slower.
+    case 8:  return launch_cfg<PwCfg<8, 8, 4, 4, 1, 4, true, 5, 4>>(c, rows);
+    case 16: return launch_cfg<PwCfg<16, 16, 4, 2, 1, 2, true, 13, 7>>(c, rows);
     // K = 32: the same with one 4-wave workgroup per CU at one wave per
-    // SIMD (fragments and accumulators need 256 VGPRs + 214 AGPRs; 6 %
-    // faster than 8-coefficient waves with a sliding A window)
-    case 32: return launch_cfg<PwCfg<32, 32, 2, 2, 1, 1, true, 1>>(c, rows);
+    // SIMD (fragments and accumulators need 256 VGPRs + 234 AGPRs; 6 %
+    // faster than 8-coefficient waves with a sliding A window); shell
+    // schedule, 7 pairs ahead, barrier after shell 24 (2 % faster than the
+    // barrier before the first MFMA with all fragments read up front)
+    case 32: return launch_cfg<PwCfg<32, 32, 2, 2, 1, 1, true, 26, 7>>(c, rows);
     default: return MFH_E_UNSUPPORTED;
     }
 }
