@@ -181,6 +181,109 @@ __device__ __forceinline__ void store_digits(int8_t *p, size_t nnp, int v)
     }
 }
 
+// The digits store_digits writes, as values (plane order)
+template <int MODE>
+__device__ __forceinline__ void digit_vals(int v, int *d)
+{
+    if constexpr (MODE == MFH_MODE_B8) {
+        d[0] = v;
+        d[1] = (v + 128) >> 8;
+        d[2] = (v + 32896) >> 16;
+    } else {
+        const int d0 = ((v + 64) & 127) - 64;
+        const int v1 = (v + 64) >> 7;
+        const int d1 = ((v1 + 64) & 127) - 64;
+        const int d2 = (v1 + 64) >> 7;
+        d[0] = d0;
+        d[1] = d1;
+        d[2] = d2;
+        d[3] = d0 + d1;
+        d[4] = d0 + d2;
+        d[5] = d1 + d2;
+    }
+}
+
+// low bytes of a, b, c, d as one dword (a lowest)
+__device__ __forceinline__ uint32_t pack4_lo(int a, int b, int c, int d)
+{
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000c0cu);
+    return lo | hi;
+}
+
+// 4 x 4 byte transpose: o[s] byte q = w[q] byte s
+__device__ __forceinline__ void transpose4x4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                             uint32_t *o)
+{
+    const uint32_t t0 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);   // w0.0 w1.0 w0.1 w1.1
+    const uint32_t t1 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);   // w0.2 w1.2 w0.3 w1.3
+    const uint32_t t2 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+    const uint32_t t3 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+    o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+
+// Staged digit stores of the forward kernels with 256 elements per
+// workgroup (which are 256 contiguous bytes of every digit plane).  A chunk
+// is 48 consecutive planes (8 ring coefficients x 6 digits, or 16 x 3):
+// every thread packs its element's 48 digit bytes into 12 dwords (group g =
+// planes 4g .. 4g+3) and writes them to LDS; after a barrier, 192 threads
+// each take one group and 16 consecutive elements, transpose the 16 x 4
+// bytes in registers and write 16 bytes to each of the group's 4 planes.
+// A wave store then covers 256 contiguous bytes of 4 planes (1 KB in 16-byte
+// pieces) instead of 64 bytes of one plane, 16 times fewer store
+// instructions.  LDS rows of 16 elements are padded to 20 dwords, so the 16
+// readers of a group (80-byte stride) hit distinct banks.
+constexpr int XCH_PLANES = 48, XCH_GROUPS = 12, XCH_ROW = 20, XCH_GSTRIDE = 16 * XCH_ROW;
+constexpr int XCH_DWORDS = XCH_GROUPS * XCH_GSTRIDE;     // one buffer: 15 KB
+
+template <int MODE>
+__device__ __forceinline__ void xch_write(uint32_t *buf, const int (&z)[XCH_PLANES / (MODE == MFH_MODE_K7 ? 6 : 3)])
+{
+    constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
+    constexpr int CPC = XCH_PLANES / PL;
+    int d[XCH_PLANES];
+#pragma unroll
+    for (int c = 0; c < CPC; ++c) digit_vals<MODE>(z[c], d + c * PL);
+    const int t = threadIdx.x;
+    uint32_t *row = buf + (t >> 4) * XCH_ROW + (t & 15);
+#pragma unroll
+    for (int g = 0; g < XCH_GROUPS; ++g)
+        row[g * XCH_GSTRIDE] = pack4_lo(d[4 * g], d[4 * g + 1], d[4 * g + 2], d[4 * g + 3]);
+}
+
+// o: the workgroup's first byte of the chunk's first plane
+__device__ __forceinline__ void xch_store(const uint32_t *buf, int8_t *o, size_t nnp)
+{
+    const int t = threadIdx.x;
+    if (t >= XCH_GROUPS * 16) return;
+    const int g = t >> 4, eb = t & 15;
+    const uint4 *src = (const uint4 *)(buf + g * XCH_GSTRIDE + eb * XCH_ROW);
+    uint32_t w[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 v = src[q];
+        w[4 * q] = v.x;
+        w[4 * q + 1] = v.y;
+        w[4 * q + 2] = v.z;
+        w[4 * q + 3] = v.w;
+    }
+    uint32_t p[4][4];          // p[s][q]: plane 4g+s, elements 4q .. 4q+3
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t o4[4];
+        transpose4x4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3], o4);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) p[s][q] = o4[s];
+    }
+    int8_t *dst = o + (size_t)(4 * g) * nnp + eb * 16;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        *(uint4 *)(dst + (size_t)s * nnp) = make_uint4(p[s][0], p[s][1], p[s][2], p[s][3]);
+}
+
 // ---- forward transform, generic plan ---------------------------------------
 // One thread per padded element (i, k) of a band of `rows` padded rows from
 // row0 of an np x np operand; it writes the digit planes of every (point j,
@@ -337,8 +440,12 @@ __device__ __forceinline__ void load_limbs(LimbsI32<L> &x, const Src &src, int i
 }
 
 // One output class q (compile time): twist + fold, length-P DIF, digits.
-template <int S, int NB, int Q, int q, int MODE, class Limbs>
-__device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t nnp)
+// XB = 0: each thread stores its element's digit bytes (o = its element in
+// plane 0); XB = 1 or 2: staged stores through XB LDS buffers of
+// XCH_DWORDS at xb (256 elements per workgroup, one thread each).
+template <int S, int NB, int Q, int q, int MODE, class Limbs, int XB = 0>
+__device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t nnp,
+                                              uint32_t *xb = nullptr)
 {
     constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
     constexpr int K = 2 * S, P = NB / Q, LS = NB / 2;
@@ -392,35 +499,59 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
         for (int bit = 1, rb = P >> 1; bit < P; bit <<= 1, rb >>= 1)
             if (pos & bit) jp |= rb;
         const int j = q + Q * jp;
+        if constexpr (XB == 0) {
 #pragma unroll
-        for (int c = 0; c < K; ++c)
-            store_digits<MODE>(o + (size_t)((j * K + c) * PL) * nnp, nnp, z[pos][c]);
+            for (int c = 0; c < K; ++c)
+                store_digits<MODE>(o + (size_t)((j * K + c) * PL) * nnp, nnp, z[pos][c]);
+        } else {
+            // chunks of CPC coefficients; chunk k of the kernel uses buffer
+            // k % XB.  One buffer: a barrier before each write (the previous
+            // chunk's readers are done) and one before the reads.  Two: the
+            // barrier before the reads of chunk k also orders every read of
+            // chunk k-1 before the writes of chunk k+1 into its buffer.
+            constexpr int CPC = XCH_PLANES / PL;
+            static_assert(K % CPC == 0, "whole chunks per point");
+            int8_t *wg = o - threadIdx.x;
+#pragma unroll
+            for (int c0 = 0; c0 < K; c0 += CPC) {
+                const int k = (q * P + pos) * (K / CPC) + c0 / CPC;
+                uint32_t *buf = xb + (k % XB) * XCH_DWORDS;
+                int zc[CPC];
+#pragma unroll
+                for (int c = 0; c < CPC; ++c) zc[c] = z[pos][c0 + c];
+                if (XB == 1 && k > 0) __syncthreads();
+                xch_write<MODE>(buf, zc);
+                __syncthreads();
+                xch_store(buf, wg + (size_t)((j * K + c0) * PL) * nnp, nnp);
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
 }
 
 // Threads of part p (p = thread / E, wave-uniform) produce the output
 // classes q = p, p + TPE, ... of their element.
-template <int S, int NB, int Q, int MODE, int TPE, int PART, class Limbs, int... is>
-__device__ __forceinline__ void forward_part(const Limbs &x, int8_t *o, size_t nnp,
+template <int S, int NB, int Q, int MODE, int TPE, int PART, class Limbs, int XB, int... is>
+__device__ __forceinline__ void forward_part(const Limbs &x, int8_t *o, size_t nnp, uint32_t *xb,
                                              std::integer_sequence<int, is...>)
 {
     // scheduling barriers between classes (and after each point's stores,
     // in forward_class): left free, the scheduler interleaves classes and
     // the S = 16 kernels need 256+ registers (140 with the barriers)
-    ((forward_class<S, NB, Q, PART + TPE * is, MODE, Limbs>(x, o, nnp),
+    ((forward_class<S, NB, Q, PART + TPE * is, MODE, Limbs, XB>(x, o, nnp, xb),
       __builtin_amdgcn_sched_barrier(0)),
      ...);
 }
-template <int S, int NB, int Q, int MODE, int TPE, class Limbs, int PART = 0>
-__device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *o, size_t nnp)
+template <int S, int NB, int Q, int MODE, int TPE, class Limbs, int XB, int PART = 0>
+__device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *o, size_t nnp,
+                                              uint32_t *xb)
 {
     if constexpr (PART < TPE) {
         if (part == PART)
-            forward_part<S, NB, Q, MODE, TPE, PART, Limbs>(x, o, nnp,
-                                                           std::make_integer_sequence<int, Q / TPE>{});
+            forward_part<S, NB, Q, MODE, TPE, PART, Limbs, XB>(
+                x, o, nnp, xb, std::make_integer_sequence<int, Q / TPE>{});
         else
-            forward_parts<S, NB, Q, MODE, TPE, Limbs, PART + 1>(part, x, o, nnp);
+            forward_parts<S, NB, Q, MODE, TPE, Limbs, XB, PART + 1>(part, x, o, nnp, xb);
     }
 }
 
@@ -431,13 +562,19 @@ __device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *
 // each plane.
 // top: limb L-1 is unsigned (0), int16 (1), or (int16)(x ^ 0x8000), i.e. the
 // entry minus 2^(16L-1) (2, recoding only).
-template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src, int E = 256>
+// XB > 0: staged digit stores through XB LDS buffers (E = 256 only; the
+// band's element count must be a multiple of 256, so every thread of every
+// workgroup has an element and reaches every barrier).
+template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src, int E = 256,
+          int XB = 0>
 __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restrict__ out, int np_,
                                                       int top_mode, int row0, int rows)
 {
     constexpr int L = NB * S / 2;
     constexpr int TPE = 256 / E;
     static_assert(E * TPE == 256 && Q % TPE == 0, "threads split evenly over classes");
+    static_assert(XB == 0 || E == 256, "staged stores: one thread per element, 256 elements");
+    __shared__ uint32_t xbuf[XB > 0 ? XB * XCH_DWORDS : 1];
     const size_t nnp = (size_t)rows * np_;           // the band's elements (plane stride)
     const size_t eband = (size_t)row0 * np_;         // its first element in the operand
     const size_t e0 = (size_t)blockIdx.x * E;
@@ -493,16 +630,16 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
                 x.top = top_s[slot];
             }
         }
-        if (e >= nnp) return;
+        if (XB == 0 && e >= nnp) return;
     } else {
-        if (e >= nnp) return;
+        if (XB == 0 && e >= nnp) return;
         int i, k;
         mfh_tile_ik(e, np_, i, k);
         i += row0;
         const bool valid = i < src.n && k < src.n;
         load_limbs<L>(x, src, i, k, valid);
     }
-    forward_parts<S, NB, Q, MODE, TPE, Limbs>(part, x, out + e, nnp);
+    forward_parts<S, NB, Q, MODE, TPE, Limbs, XB>(part, x, out + e, nnp, xbuf);
 }
 
 // |limb| <= 65535 for int32 inputs (the transform and digit bounds assume it)
@@ -1012,30 +1149,39 @@ int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
 namespace {
 // compile-time plans: (S, NB) with Q output classes of length NB/Q
 template <int S, int NB, int MODE, bool RECODE, class Src, class Limbs, int E = 256,
-          int Q = NB / 4>
+          int Q = NB / 4, int XB = 0>
 bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_mode, int row0, int rows)
 {
     if (c->S != S || c->NB != NB || c->mode != MODE || (c->recode != 0) != RECODE) return false;
     if (top_mode == 2 && !RECODE) return false;
     const size_t nnp = (size_t)rows * c->np;
-    hipLaunchKernelGGL((k_forward_fast<S, NB, Q, MODE, RECODE, Limbs, Src, E>),
+    if (XB > 0 && nnp % E) return false;     // staged stores need whole workgroups
+    hipLaunchKernelGGL((k_forward_fast<S, NB, Q, MODE, RECODE, Limbs, Src, E, XB>),
                        dim3((unsigned)((nnp + E - 1) / E)), dim3(256), 0, c->stream, s, dst,
                        c->np, top_mode, row0, rows);
     return true;
 }
 
+// Plans with 256 elements per workgroup store their digits through LDS
+// (XB = 1): forward 2.04 -> 1.77 ms at W = 2048 (both operands and the B
+// transpose), 9.7 -> 6.2 ms at W = 512 and n = 4096, 1.71 -> 1.1 ms for
+// fp32 at n = 2048; two buffers (one barrier per chunk) measured equal or
+// slower.
 bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, int rows)
 {
     constexpr int K7 = MFH_MODE_K7, B8 = MFH_MODE_B8;
     if (c->n % 8) return false;   // staged 16-byte loads need rows of 8k limbs
-    return try_fast<8, 32, K7, true, SrcU16, LimbsLds<128>>(c, s, dst, ts, r0, rows) ||  // W=2048
-           try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>>(c, s, dst, ts, r0, rows) ||
-           try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>>(c, s, dst, ts, r0, rows) ||  // W=1024
+    return try_fast<8, 32, K7, true, SrcU16, LimbsLds<128>, 256, 8, 1>(c, s, dst, ts, r0,
+                                                                       rows) ||  // W=2048
+           try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>, 256, 8, 1>(c, s, dst, ts, r0, rows) ||
+           try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>, 256, 4, 1>(c, s, dst, ts, r0,
+                                                                       rows) ||  // W=1024
            try_fast<16, 64, K7, true, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst, ts, r0,
                                                                         rows) ||    // W=8192
            try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst, ts, r0,
                                                                          rows) ||
-           try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>>(c, s, dst, ts, r0, rows) ||  // W=512
+           try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>, 256, 4, 1>(c, s, dst, ts, r0,
+                                                                       rows) ||  // W=512
            try_fast<16, 32, K7, false, SrcU16, LimbsLds<256, 64>, 64, 16>(c, s, dst, ts, r0,
                                                                          rows);    // W=4096
 }
@@ -1079,8 +1225,8 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
             done = forward_fast_u16(c, s, dst, top, r0, rows);
         } else if (in_kind == MFH_IN_F32) {
             SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
-            done = try_fast<4, 16, MFH_MODE_K7, false, SrcF32, LimbsI32<32>>(c, s, dst, 0, r0,
-                                                                            rows);
+            done = try_fast<4, 16, MFH_MODE_K7, false, SrcF32, LimbsI32<32>, 256, 4, 1>(
+                c, s, dst, 0, r0, rows);
         }
         if (done) {
             MFH_HIP(hipGetLastError());
