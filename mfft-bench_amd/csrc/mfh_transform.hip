@@ -1052,6 +1052,43 @@ __global__ __launch_bounds__(256) void k_encode(Src src, int32_t *__restrict__ o
 }
 
 // ---- plane transpose (B operand) -----------------------------------------------
+// uint16 planes with n a multiple of 64 (whole 64 x 64 tiles): 16-byte
+// loads of 8 consecutive elements of a row, 16-byte stores of 8 consecutive
+// elements of a column gathered from LDS (rows padded to 66 elements: the 8
+// rows a lane gathers fall in distinct banks)
+__global__ __launch_bounds__(256) void k_transpose_u16x8(const uint4 *__restrict__ src,
+                                                        uint4 *__restrict__ dst, int n)
+{
+    __shared__ uint16_t tile[64][66];
+    const size_t nn = (size_t)n * n;
+    const uint16_t *s = (const uint16_t *)src + (size_t)blockIdx.z * nn;
+    uint16_t *d = (uint16_t *)dst + (size_t)blockIdx.z * nn;
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int q = threadIdx.x + 256 * k;           // 512 chunks of 8
+        const int r = q >> 3, c8 = (q & 7) * 8;
+        const uint4 v = *(const uint4 *)(s + (size_t)(r0 + r) * n + c0 + c8);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            tile[r][c8 + 2 * e] = (uint16_t)(w[e] & 0xFFFFu);
+            tile[r][c8 + 2 * e + 1] = (uint16_t)(w[e] >> 16);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int q = threadIdx.x + 256 * k;
+        const int c = q >> 3, r8 = (q & 7) * 8;       // dst row c0 + c, cols r0 + r8 ..
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w[e] = (uint32_t)tile[r8 + 2 * e][c] | ((uint32_t)tile[r8 + 2 * e + 1][c] << 16);
+        *(uint4 *)(d + (size_t)(c0 + c) * n + r0 + r8) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 template <class T>
 __global__ __launch_bounds__(256) void k_transpose(const T *__restrict__ src,
                                                    T *__restrict__ dst, int n)
@@ -1131,7 +1168,10 @@ int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
                          int elem_bytes, hipStream_t st)
 {
     dim3 grid((n + 63) / 64, (n + 63) / 64, planes);
-    if (elem_bytes == 2)
+    if (elem_bytes == 2 && n % 64 == 0 && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0)
+        hipLaunchKernelGGL(k_transpose_u16x8, grid, dim3(256), 0, st, (const uint4 *)src,
+                           (uint4 *)dst, n);
+    else if (elem_bytes == 2)
         hipLaunchKernelGGL(k_transpose<uint16_t>, grid, dim3(256), 0, st,
                            (const uint16_t *)src, (uint16_t *)dst, n);
     else if (elem_bytes == 4)
