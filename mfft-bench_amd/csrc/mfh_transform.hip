@@ -236,31 +236,38 @@ __device__ __forceinline__ void transpose4x4(uint32_t w0, uint32_t w1, uint32_t 
 // pieces) instead of 64 bytes of one plane, 16 times fewer store
 // instructions.  LDS rows of 16 elements are padded to 20 dwords, so the 16
 // readers of a group (80-byte stride) hit distinct banks.
-constexpr int XCH_PLANES = 48, XCH_GROUPS = 12, XCH_ROW = 20, XCH_GSTRIDE = 16 * XCH_ROW;
-constexpr int XCH_DWORDS = XCH_GROUPS * XCH_GSTRIDE;     // one buffer: 15 KB
+// The same with NE = 64 elements staged by one wave in a private buffer
+// (the 4096- and 8192-bit plans: 64 elements per workgroup, each wave
+// computing a quarter of the output classes for all of them): 48 lanes
+// store, no workgroup barrier.
+constexpr int XCH_PLANES = 48, XCH_GROUPS = 12, XCH_ROW = 20;
+constexpr int XCH_DWORDS = XCH_GROUPS * 16 * XCH_ROW;     // 256 elements: 15 KB
 
-template <int MODE>
-__device__ __forceinline__ void xch_write(uint32_t *buf, const int (&z)[XCH_PLANES / (MODE == MFH_MODE_K7 ? 6 : 3)])
+// t: this thread's element among the NE
+template <int MODE, int NE>
+__device__ __forceinline__ void xch_write(uint32_t *buf, const int (&z)[XCH_PLANES / (MODE == MFH_MODE_K7 ? 6 : 3)],
+                                          int t)
 {
     constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
     constexpr int CPC = XCH_PLANES / PL;
+    constexpr int GSTRIDE = (NE / 16) * XCH_ROW;
     int d[XCH_PLANES];
 #pragma unroll
     for (int c = 0; c < CPC; ++c) digit_vals<MODE>(z[c], d + c * PL);
-    const int t = threadIdx.x;
     uint32_t *row = buf + (t >> 4) * XCH_ROW + (t & 15);
 #pragma unroll
     for (int g = 0; g < XCH_GROUPS; ++g)
-        row[g * XCH_GSTRIDE] = pack4_lo(d[4 * g], d[4 * g + 1], d[4 * g + 2], d[4 * g + 3]);
+        row[g * GSTRIDE] = pack4_lo(d[4 * g], d[4 * g + 1], d[4 * g + 2], d[4 * g + 3]);
 }
 
-// o: the workgroup's first byte of the chunk's first plane
-__device__ __forceinline__ void xch_store(const uint32_t *buf, int8_t *o, size_t nnp)
+// o: the first byte of the NE elements in the chunk's first plane
+template <int NE>
+__device__ __forceinline__ void xch_store(const uint32_t *buf, int8_t *o, size_t nnp, int t)
 {
-    const int t = threadIdx.x;
-    if (t >= XCH_GROUPS * 16) return;
-    const int g = t >> 4, eb = t & 15;
-    const uint4 *src = (const uint4 *)(buf + g * XCH_GSTRIDE + eb * XCH_ROW);
+    constexpr int EB = NE / 16, GSTRIDE = EB * XCH_ROW;
+    if (t >= XCH_GROUPS * EB) return;
+    const int g = t / EB, eb = t % EB;
+    const uint4 *src = (const uint4 *)(buf + g * GSTRIDE + eb * XCH_ROW);
     uint32_t w[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -442,7 +449,9 @@ __device__ __forceinline__ void load_limbs(LimbsI32<L> &x, const Src &src, int i
 // One output class q (compile time): twist + fold, length-P DIF, digits.
 // XB = 0: each thread stores its element's digit bytes (o = its element in
 // plane 0); XB = 1 or 2: staged stores through XB LDS buffers of
-// XCH_DWORDS at xb (256 elements per workgroup, one thread each).
+// XCH_DWORDS at xb (256 elements per workgroup, one thread each); XB = 3:
+// staged per wave (64 elements per workgroup, wave w's buffer at
+// xb + w * XCH_DWORDS / 4).
 template <int S, int NB, int Q, int q, int MODE, class Limbs, int XB = 0>
 __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t nnp,
                                               uint32_t *xb = nullptr)
@@ -503,6 +512,26 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
 #pragma unroll
             for (int c = 0; c < K; ++c)
                 store_digits<MODE>(o + (size_t)((j * K + c) * PL) * nnp, nnp, z[pos][c]);
+        } else if constexpr (XB == 3) {
+            // the wave's own buffer: LDS operations of one wave complete in
+            // order; the memory clobbers keep the compiler from moving the
+            // other lanes' reads above the writes, or the next chunk's writes
+            // above this chunk's reads
+            constexpr int CPC = XCH_PLANES / PL;
+            static_assert(K % CPC == 0, "whole chunks per point");
+            const int lane = threadIdx.x & 63;
+            uint32_t *buf = xb + (threadIdx.x >> 6) * (XCH_DWORDS / 4);
+            int8_t *wg = o - lane;
+#pragma unroll
+            for (int c0 = 0; c0 < K; c0 += CPC) {
+                int zc[CPC];
+#pragma unroll
+                for (int c = 0; c < CPC; ++c) zc[c] = z[pos][c0 + c];
+                asm volatile("" ::: "memory");
+                xch_write<MODE, 64>(buf, zc, lane);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                xch_store<64>(buf, wg + (size_t)((j * K + c0) * PL) * nnp, nnp, lane);
+            }
         } else {
             // chunks of CPC coefficients; chunk k of the kernel uses buffer
             // k % XB.  One buffer: a barrier before each write (the previous
@@ -520,9 +549,9 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
 #pragma unroll
                 for (int c = 0; c < CPC; ++c) zc[c] = z[pos][c0 + c];
                 if (XB == 1 && k > 0) __syncthreads();
-                xch_write<MODE>(buf, zc);
+                xch_write<MODE, 256>(buf, zc, threadIdx.x);
                 __syncthreads();
-                xch_store(buf, wg + (size_t)((j * K + c0) * PL) * nnp, nnp);
+                xch_store<256>(buf, wg + (size_t)((j * K + c0) * PL) * nnp, nnp, threadIdx.x);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -573,8 +602,9 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
     constexpr int L = NB * S / 2;
     constexpr int TPE = 256 / E;
     static_assert(E * TPE == 256 && Q % TPE == 0, "threads split evenly over classes");
-    static_assert(XB == 0 || E == 256, "staged stores: one thread per element, 256 elements");
-    __shared__ uint32_t xbuf[XB > 0 ? XB * XCH_DWORDS : 1];
+    static_assert(XB == 0 || (XB < 3 && E == 256) || (XB == 3 && E == 64),
+                  "staged stores: 256 elements per workgroup, or 64 per wave");
+    __shared__ uint32_t xbuf[XB == 3 ? XCH_DWORDS : XB > 0 ? XB * XCH_DWORDS : 1];
     const size_t nnp = (size_t)rows * np_;           // the band's elements (plane stride)
     const size_t eband = (size_t)row0 * np_;         // its first element in the operand
     const size_t e0 = (size_t)blockIdx.x * E;
@@ -1216,14 +1246,14 @@ bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, 
            try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>, 256, 8, 1>(c, s, dst, ts, r0, rows) ||
            try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>, 256, 4, 1>(c, s, dst, ts, r0,
                                                                        rows) ||  // W=1024
-           try_fast<16, 64, K7, true, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst, ts, r0,
-                                                                        rows) ||    // W=8192
-           try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32>(c, s, dst, ts, r0,
-                                                                         rows) ||
+           try_fast<16, 64, K7, true, SrcU16, LimbsLds<512, 64>, 64, 32, 3>(c, s, dst, ts, r0,
+                                                                           rows) ||  // W=8192
+           try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32, 3>(c, s, dst, ts, r0,
+                                                                            rows) ||
            try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>, 256, 4, 1>(c, s, dst, ts, r0,
                                                                        rows) ||  // W=512
-           try_fast<16, 32, K7, false, SrcU16, LimbsLds<256, 64>, 64, 16>(c, s, dst, ts, r0,
-                                                                         rows);    // W=4096
+           try_fast<16, 32, K7, false, SrcU16, LimbsLds<256, 64>, 64, 16, 3>(c, s, dst, ts, r0,
+                                                                            rows);  // W=4096
 }
 }  // namespace
 
