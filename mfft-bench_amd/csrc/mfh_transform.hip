@@ -135,22 +135,29 @@ struct SrcF64 {
 
 // C^ from the pointwise step's int32 class results (`cs` ints between
 // classes): B8 sum_m class_m 2^(8m); K7 the Karatsuba recombination
+// NT: stream the class values past the caches (each is read once)
+template <bool NT = true>
+__device__ __forceinline__ int ld_cls(const int32_t *p)
+{
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+template <bool NT = true>
 __device__ __forceinline__ long long combine_classes(const int32_t *p, size_t cs, int mode)
 {
     if (mode == MFH_MODE_K7) {
-        // each class value is read once: stream it past the caches
-        const long long P0 = __builtin_nontemporal_load(p), P1 = __builtin_nontemporal_load(p + cs),
-                        P2 = __builtin_nontemporal_load(p + 2 * cs),
-                        P3 = __builtin_nontemporal_load(p + 3 * cs),
-                        P4 = __builtin_nontemporal_load(p + 4 * cs),
-                        P5 = __builtin_nontemporal_load(p + 5 * cs);
+        const long long P0 = ld_cls<NT>(p), P1 = ld_cls<NT>(p + cs),
+                        P2 = ld_cls<NT>(p + 2 * cs),
+                        P3 = ld_cls<NT>(p + 3 * cs),
+                        P4 = ld_cls<NT>(p + 4 * cs),
+                        P5 = ld_cls<NT>(p + 5 * cs);
         const long long c1 = P3 - P0 - P1, c2 = P4 - P0 - P2 + P1, c3 = P5 - P1 - P2;
         return P0 + c1 * 128 + c2 * 16384 + c3 * 2097152 + P2 * 268435456;
     }
     long long v = 0;
 #pragma unroll
     for (int m = MFH_CLASSES - 1; m >= 0; --m)
-        v = v * 256 + (long long)__builtin_nontemporal_load(p + m * cs);
+        v = v * 256 + (long long)ld_cls<NT>(p + m * cs);
     return v;
 }
 
@@ -778,7 +785,12 @@ __device__ __forceinline__ long long bperm64(long long v, int addr)
 // r_i / s_j the sums of row i of A-hJ / column j of B-hJ.  With
 // r_i = sum_u rowS[u][i] 2^(16u) (likewise s_j), h r_i adds
 // rowS[u][i] 2^15 to plane L-1+u, and h^2 n adds n 2^14 to plane 2L-1.
-template <int NB, int K, bool CARRY, int NPASS = 2>
+// NT: class loads past the caches.  Plain loads measured faster only for
+// the fused W = 2048 plan (NB = 32, K = 16: 3.07 -> 2.90 ms); elsewhere
+// (fused NB = 16 K = 8 and NB = 64 K = 32, and without the fused carry)
+// non-temporal loads were 3-4 % faster.
+template <int NB, int K, bool CARRY, int NPASS = 2,
+          bool NT = !(CARRY && NB == 32 && K == 16)>
 __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict__ C5,
                                                       int64_t *__restrict__ Cw,
                                                       uint16_t *__restrict__ out, int RL,
@@ -810,7 +822,7 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
 #pragma unroll
             for (int bit = 1, rb = NB >> 1; bit < NB; bit <<= 1, rb >>= 1)
                 if (j & bit) r |= rb;
-            X[r] = valid ? combine_classes(C5 + mfh_c5_index(j, i, jj, c, np_, ncl, K, rows),
+            X[r] = valid ? combine_classes<NT>(C5 + mfh_c5_index(j, i, jj, c, np_, ncl, K, rows),
                                            mfh_c5_class_stride(np_, K), mode)
                          : 0;
         }
