@@ -89,6 +89,8 @@ int mfh_conv(mfh_ctx *ctx, const int32_t *A32, const int32_t *B32,
              int64_t *Cw);
 
 /* ---- device-buffer entry points (stream-ordered, no sync) --------------- */
+/* dA and dB must be 16-byte aligned (the limbs are read 8 at a time; any
+ * hipMalloc pointer is): MFH_E_ARG otherwise, before any kernel runs. */
 int mfh_mm_dev(mfh_ctx *ctx, int in_kind, const void *dA, const void *dB,
                void *dOut, int RL);
 int mfh_conv_dev(mfh_ctx *ctx, const void *dA32, const void *dB32, void *dCw);

@@ -326,6 +326,8 @@ int mfh_band_rows(const mfh_ctx *c) { return c ? c->hb : MFH_E_ARG; }
 int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut, int RL)
 {
     if (!c || !dA || !dB || !dOut || RL < 1) return MFH_E_ARG;
+    // the forward kernels stage limbs with 16-byte loads
+    if (((uintptr_t)dA | (uintptr_t)dB) % 16) return MFH_E_ARG;
     if (kind != MFH_IN_U16 && kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
     select_mode(c, kind);
     int carried = 0;

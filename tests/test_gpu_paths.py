@@ -51,6 +51,20 @@ def test_conv_rejects_out_of_range_limb(gpu):
     assert e.value.code == -5
 
 
+def test_mm_dev_rejects_unaligned_limbs(gpu, lib):
+    """mfh_mm_dev reads limbs 8 at a time: a device pointer that is not
+    16-byte aligned is refused before any kernel runs."""
+    n, L = 8, 16
+    with gpu.Ctx(n, L) as ctx:
+        dA = gpu.DevBuf(L * n * n * 2 + 16)
+        dO = gpu.DevBuf((2 * L + 1) * n * n * 2)
+        off = C.c_void_p(dA.ptr.value + 2)
+        rc = lib.mfh_mm_dev(ctx.h, 0, off, dA.ptr, dO.ptr, 2 * L + 1)
+        for b in (dA, dO):
+            b.free()
+    assert rc == -3                      # MFH_E_ARG
+
+
 def test_c_api_conv_mfft(gpu, orc):
     n, L = 12, 32
     rng = np.random.default_rng(1)
