@@ -136,6 +136,11 @@ struct mfh_ctx {
     // last product: output kind (0 limbs, 1 coefficient planes, 2 fp32),
     // output limbs, whether the carry ran inside the inverse kernel
     int last_out, last_RL, last_fused;
+    // set by the float entry points around a product: the inverse kernels
+    // that can decode into fp32 / fp64 (MFH_DEC_* + 1; 0 = none) do so,
+    // writing dec_out with scale 2^-dec_SAB, instead of writing Cw
+    int dec_req, dec_SAB;
+    void *dec_out;
     // timing: ev[0] start, ev[4] end; per row band b, bev[b][0..3] before
     // A's forward transform, after it, after the pointwise step, after the
     // inverse (nbands of them)

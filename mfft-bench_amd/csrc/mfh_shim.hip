@@ -372,12 +372,21 @@ int fpx_mm_dev(mfh_ctx *c, int f64, const void *dA, const void *dB, int SA, int 
     if (!c || !dA || !dB || !dC) return MFH_E_ARG;
     if (!conv_size_ok(c)) return MFH_E_BOUND;
     select_mode(c, -1);
-    int rc = run_conv(c, f64 ? MFH_IN_F64 : MFH_IN_F32, dA, dB, c->dCw, SA, SB);
+    // the specialised inverse kernels decode straight from their planes
+    c->dec_req = (f64 ? MFH_DEC_F64 : MFH_DEC_F32) + 1;
+    c->dec_out = dC;
+    c->dec_SAB = SA + SB;
+    int decoded = 0;
+    int rc = run_conv(c, f64 ? MFH_IN_F64 : MFH_IN_F32, dA, dB, c->dCw, SA, SB, nullptr, 0,
+                      &decoded);
+    c->dec_req = 0;
+    c->dec_out = nullptr;
     if (rc) return rc;
-    if ((rc = mfh_launch_decode(c, c->dCw, SA + SB, f64 ? MFH_DEC_F64 : MFH_DEC_F32, dC,
+    if (decoded != 2 &&
+        (rc = mfh_launch_decode(c, c->dCw, SA + SB, f64 ? MFH_DEC_F64 : MFH_DEC_F32, dC,
                                 nullptr)))
         return rc;
-    c->last_out = f64 ? 3 : 2; c->last_fused = 0;
+    c->last_out = f64 ? 3 : 2; c->last_fused = decoded == 2;
     mark(c, 4);
     return MFH_OK;
 }

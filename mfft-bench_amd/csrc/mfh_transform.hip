@@ -773,6 +773,109 @@ __device__ __forceinline__ long long bperm64(long long v, int addr)
     return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
 }
 
+// ---- fixed-point decode (src/fpfixed.c:212-322) ------------------------------
+// Carry over RL = 2L+2 limbs with an arithmetic shift, take the magnitude
+// (two's complement negation when the final carry is negative), keep the
+// top <= 4 limbs below the highest non-zero one plus a sticky bit, round to
+// 24 bits half-even, and scale by 2^-(SA+SB).  Exact zero gives +0.0f.
+// Streaming: both the value and its negation are tracked limb by limb, so no
+// per-element limb array is needed.
+struct TopTrack {
+    int h;
+    uint32_t hist[4];      // limbs w-3 .. w
+    uint32_t win[4];       // limbs h-3 .. h when h was set
+    uint32_t below;        // OR of limbs < w-3
+    uint32_t sticky;       // OR of limbs < h-3 when h was set
+    __device__ void init()
+    {
+        h = -1; below = 0; sticky = 0;
+        for (int q = 0; q < 4; ++q) { hist[q] = 0; win[q] = 0; }
+    }
+    __device__ void push(int w, uint32_t limb)
+    {
+        below |= hist[0];
+        hist[0] = hist[1]; hist[1] = hist[2]; hist[2] = hist[3]; hist[3] = limb;
+        if (limb) {
+            h = w;
+            for (int q = 0; q < 4; ++q) win[q] = hist[q];
+            sticky = below;
+        }
+    }
+};
+
+// FMT: MFH_DEC_F32 rounds to 24 bits and writes fp32, MFH_DEC_F64 to 53
+// bits and fp64 (src/fpfixed.c:308-322), MFH_DEC_SIG63 to 63 bits and writes
+// the signed significand and the exponent of the long double decode
+// (src/fpfixed.c:292-306: int64 sig at out, int32 exponent at out2).
+// Decode of one element from its 2L-1 coefficient planes (plane(w), w < P)
+// over RL limbs (src/fpfixed.c:212-322, see k_decode)
+template <int FMT, class Plane>
+__device__ __forceinline__ void decode_value(const Plane &plane, int P, int RL, int SAB,
+                                             void *__restrict__ out_, int32_t *__restrict__ out2,
+                                             size_t e)
+{
+    constexpr int BITS = FMT == MFH_DEC_F32 ? 24 : FMT == MFH_DEC_F64 ? 53 : 63;
+    TopTrack pos, neg;
+    pos.init(); neg.init();
+    int64_t carry = 0;
+    uint32_t borrow = 1;
+    for (int w = 0; w < RL; ++w) {
+        int64_t t = carry + (w < P ? plane(w) : 0);
+        uint32_t limb = (uint32_t)(t & 0xFFFF);
+        carry = t >> 16;
+        uint32_t nl = ((~limb) & 0xFFFFu) + borrow;
+        borrow = nl >> 16;
+        nl &= 0xFFFFu;
+        pos.push(w, limb);
+        neg.push(w, nl);
+    }
+    const bool isneg = carry < 0;
+    const int h = isneg ? neg.h : pos.h;
+    if (h < 0) {
+        if constexpr (FMT == MFH_DEC_F32) ((float *)out_)[e] = 0.0f;
+        else if constexpr (FMT == MFH_DEC_F64) ((double *)out_)[e] = 0.0;
+        else { ((long long *)out_)[e] = 0; out2[e] = 0; }
+        return;
+    }
+    uint32_t win[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) win[q] = isneg ? neg.win[q] : pos.win[q];
+    const uint32_t sticky = isneg ? neg.sticky : pos.sticky;
+    int bl = 32 - __clz(win[3]);
+    const int k = h + 1 < 4 ? h + 1 : 4;
+    unsigned long long top = 0;
+#pragma unroll
+    for (int q = 3; q >= 0; --q)
+        if (q > 3 - k) top = (top << 16) | win[q];
+    // limbs below the gathered ones: win[0 .. 3-k] (positions h-3 .. h-k)
+    // only exist when k == 4, so sticky is the OR below h-3.
+    const int base = 16 * (h - k + 1);
+    int tb = 16 * h + bl - base;
+    int shift = base;
+    unsigned long long sig = top;
+    // a window of at most BITS bits is returned as it stands (sticky unused)
+    if (tb > BITS) {
+        int drop = tb - BITS;
+        sig = top >> drop;
+        unsigned long long rem = top & ((1ULL << drop) - 1);
+        unsigned long long half = 1ULL << (drop - 1);
+        int up = rem > half ? 1 : rem < half ? 0 : (sticky ? 1 : (int)(sig & 1));
+        sig += (unsigned long long)up;
+        if (sig >> BITS) { sig >>= 1; drop++; }
+        shift += drop;
+    }
+    if constexpr (FMT == MFH_DEC_F32) {
+        float v = ldexpf((float)sig, shift - SAB);
+        ((float *)out_)[e] = isneg ? -v : v;
+    } else if constexpr (FMT == MFH_DEC_F64) {
+        double v = ldexp((double)sig, shift - SAB);
+        ((double *)out_)[e] = isneg ? -v : v;
+    } else {
+        ((long long *)out_)[e] = isneg ? -(long long)sig : (long long)sig;
+        out2[e] = shift - SAB;
+    }
+}
+
 //
 // CARRY: instead of writing Cw, one thread per element (all in the first
 // wave, E <= 64) propagates the carries through the element's 2L-1 planes
@@ -789,16 +892,21 @@ __device__ __forceinline__ long long bperm64(long long v, int addr)
 // the fused W = 2048 plan (NB = 32, K = 16: 3.07 -> 2.90 ms); elsewhere
 // (fused NB = 16 K = 8 and NB = 64 K = 32, and without the fused carry)
 // non-temporal loads were 3-4 % faster.
+// DEC >= 0 (CARRY false): instead of writing Cw, one thread per element
+// decodes the element's planes from LDS into fp32 / fp64 (MFH_DEC_*) at
+// dec_out with scale 2^-SAB (the semantics of k_decode).
 template <int NB, int K, bool CARRY, int NPASS = 2,
-          bool NT = !(CARRY && NB == 32 && K == 16)>
+          bool NT = !(CARRY && NB == 32 && K == 16), int DEC = -1>
 __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict__ C5,
                                                       int64_t *__restrict__ Cw,
                                                       uint16_t *__restrict__ out, int RL,
                                                       int n, int np_, int P, int mode, int ncl,
                                                       size_t eb0, size_t eb1, int r0, int rows,
                                                       const int64_t *__restrict__ rowS,
-                                                      const int64_t *__restrict__ colS)
+                                                      const int64_t *__restrict__ colS,
+                                                      void *__restrict__ dec_out, int SAB)
 {
+    static_assert(DEC < 0 || !CARRY, "decode replaces the Cw output");
     constexpr int S = K / 2, g = 2 * K / NB, twoK = 2 * K;
     constexpr int PASS = 256 / K;            // elements per pass
     constexpr int E = NPASS * PASS;          // elements per workgroup
@@ -929,6 +1037,10 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
                 cc = v >> 16;
             }
         }
+    } else if constexpr (DEC >= 0) {
+        if (tid < ecount)
+            decode_value<DEC>([&](int w) { return cwl[(size_t)w * E + tid]; }, P, P + 3, SAB,
+                              dec_out, nullptr, e0 + tid);
     } else {
         for (int idx = tid; idx < P * E; idx += 256) {
             const int w = idx / E, el = idx % E;
@@ -970,108 +1082,16 @@ __global__ __launch_bounds__(256) void k_offset_sums(const uint16_t *__restrict_
     if (lane == 0) out[row] = acc;
 }
 
-// ---- fixed-point decode (src/fpfixed.c:212-322) ------------------------------
-// Carry over RL = 2L+2 limbs with an arithmetic shift, take the magnitude
-// (two's complement negation when the final carry is negative), keep the
-// top <= 4 limbs below the highest non-zero one plus a sticky bit, round to
-// 24 bits half-even, and scale by 2^-(SA+SB).  Exact zero gives +0.0f.
-// Streaming: both the value and its negation are tracked limb by limb, so no
-// per-element limb array is needed.
-struct TopTrack {
-    int h;
-    uint32_t hist[4];      // limbs w-3 .. w
-    uint32_t win[4];       // limbs h-3 .. h when h was set
-    uint32_t below;        // OR of limbs < w-3
-    uint32_t sticky;       // OR of limbs < h-3 when h was set
-    __device__ void init()
-    {
-        h = -1; below = 0; sticky = 0;
-        for (int q = 0; q < 4; ++q) { hist[q] = 0; win[q] = 0; }
-    }
-    __device__ void push(int w, uint32_t limb)
-    {
-        below |= hist[0];
-        hist[0] = hist[1]; hist[1] = hist[2]; hist[2] = hist[3]; hist[3] = limb;
-        if (limb) {
-            h = w;
-            for (int q = 0; q < 4; ++q) win[q] = hist[q];
-            sticky = below;
-        }
-    }
-};
 
-// FMT: MFH_DEC_F32 rounds to 24 bits and writes fp32, MFH_DEC_F64 to 53
-// bits and fp64 (src/fpfixed.c:308-322), MFH_DEC_SIG63 to 63 bits and writes
-// the signed significand and the exponent of the long double decode
-// (src/fpfixed.c:292-306: int64 sig at out, int32 exponent at out2).
 template <int FMT>
 __global__ __launch_bounds__(256) void k_decode(const int64_t *__restrict__ Cw,
                                                 void *__restrict__ out_,
                                                 int32_t *__restrict__ out2,
                                                 size_t nn, int P, int RL, int SAB)
 {
-    constexpr int BITS = FMT == MFH_DEC_F32 ? 24 : FMT == MFH_DEC_F64 ? 53 : 63;
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= nn) return;
-    TopTrack pos, neg;
-    pos.init(); neg.init();
-    int64_t carry = 0;
-    uint32_t borrow = 1;
-    for (int w = 0; w < RL; ++w) {
-        int64_t t = carry + (w < P ? Cw[(size_t)w * nn + e] : 0);
-        uint32_t limb = (uint32_t)(t & 0xFFFF);
-        carry = t >> 16;
-        uint32_t nl = ((~limb) & 0xFFFFu) + borrow;
-        borrow = nl >> 16;
-        nl &= 0xFFFFu;
-        pos.push(w, limb);
-        neg.push(w, nl);
-    }
-    const bool isneg = carry < 0;
-    const int h = isneg ? neg.h : pos.h;
-    if (h < 0) {
-        if constexpr (FMT == MFH_DEC_F32) ((float *)out_)[e] = 0.0f;
-        else if constexpr (FMT == MFH_DEC_F64) ((double *)out_)[e] = 0.0;
-        else { ((long long *)out_)[e] = 0; out2[e] = 0; }
-        return;
-    }
-    uint32_t win[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) win[q] = isneg ? neg.win[q] : pos.win[q];
-    const uint32_t sticky = isneg ? neg.sticky : pos.sticky;
-    int bl = 32 - __clz(win[3]);
-    const int k = h + 1 < 4 ? h + 1 : 4;
-    unsigned long long top = 0;
-#pragma unroll
-    for (int q = 3; q >= 0; --q)
-        if (q > 3 - k) top = (top << 16) | win[q];
-    // limbs below the gathered ones: win[0 .. 3-k] (positions h-3 .. h-k)
-    // only exist when k == 4, so sticky is the OR below h-3.
-    const int base = 16 * (h - k + 1);
-    int tb = 16 * h + bl - base;
-    int shift = base;
-    unsigned long long sig = top;
-    // a window of at most BITS bits is returned as it stands (sticky unused)
-    if (tb > BITS) {
-        int drop = tb - BITS;
-        sig = top >> drop;
-        unsigned long long rem = top & ((1ULL << drop) - 1);
-        unsigned long long half = 1ULL << (drop - 1);
-        int up = rem > half ? 1 : rem < half ? 0 : (sticky ? 1 : (int)(sig & 1));
-        sig += (unsigned long long)up;
-        if (sig >> BITS) { sig >>= 1; drop++; }
-        shift += drop;
-    }
-    if constexpr (FMT == MFH_DEC_F32) {
-        float v = ldexpf((float)sig, shift - SAB);
-        ((float *)out_)[e] = isneg ? -v : v;
-    } else if constexpr (FMT == MFH_DEC_F64) {
-        double v = ldexp((double)sig, shift - SAB);
-        ((double *)out_)[e] = isneg ? -v : v;
-    } else {
-        ((long long *)out_)[e] = isneg ? -(long long)sig : (long long)sig;
-        out2[e] = shift - SAB;
-    }
+    decode_value<FMT>([&](int w) { return Cw[(size_t)w * nn + e]; }, P, RL, SAB, out_, out2, e);
 }
 
 // ---- fp32 / fp64 encode into limb planes (src/fpfixed.c:144-204) ------------
@@ -1360,7 +1380,7 @@ int mfh_launch_check_i32(mfh_ctx *c, const int32_t *src, int planes)
 }
 
 namespace {
-template <int NB, int K, bool CARRY, int NPASS = 2>
+template <int NB, int K, bool CARRY, int NPASS = 2, int DEC = -1>
 bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, size_t eb0,
                          size_t eb1, int r0, int rows)
 {
@@ -1371,17 +1391,19 @@ bool try_inverse_fast_as(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, size_t 
     if (lds > 160 * 1024) return false;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)k_inverse_fast<NB, K, CARRY, NPASS>,
+        if (hipFuncSetAttribute((const void *)k_inverse_fast<NB, K, CARRY, NPASS,
+                                                             !(CARRY && NB == 32 && K == 16), DEC>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize,
                                 160 * 1024) != hipSuccess)
             return false;
         attr_set = true;
     }
-    hipLaunchKernelGGL((k_inverse_fast<NB, K, CARRY, NPASS>),
+    hipLaunchKernelGGL((k_inverse_fast<NB, K, CARRY, NPASS, !(CARRY && NB == 32 && K == 16),
+                                       DEC>),
                        dim3((unsigned)((eb1 - eb0 + E - 1) / E)), dim3(256), lds, c->stream,
                        c->dC5, Cw, out, RL, c->n, c->np, P, c->mode, mfh_nclasses(c->mode), eb0,
                        eb1, r0, rows, c->offset ? c->dRow : nullptr,
-                       c->offset ? c->dCol : nullptr);
+                       c->offset ? c->dCol : nullptr, c->dec_out, c->dec_SAB);
     return true;
 }
 // out != nullptr: fused carry into RL uint16 limbs (Cw is not written).
@@ -1396,6 +1418,12 @@ bool try_inverse_fast(mfh_ctx *c, int64_t *Cw, uint16_t *&out, int RL, size_t eb
     if (c->NB != NB || c->K != K) return false;
     if (out) return try_inverse_fast_as<NB, K, true, 1>(c, Cw, out, RL, eb0, eb1, r0, rows);
     out = nullptr;
+    if (c->dec_req == MFH_DEC_F32 + 1)
+        return try_inverse_fast_as<NB, K, false, 2, MFH_DEC_F32>(c, Cw, out, RL, eb0, eb1, r0,
+                                                                 rows);
+    if (c->dec_req == MFH_DEC_F64 + 1)
+        return try_inverse_fast_as<NB, K, false, 2, MFH_DEC_F64>(c, Cw, out, RL, eb0, eb1, r0,
+                                                                 rows);
     return try_inverse_fast_as<NB, K, false>(c, Cw, out, RL, eb0, eb1, r0, rows);
 }
 }  // namespace
@@ -1415,7 +1443,8 @@ int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carr
          try_inverse_fast<16, 8>(c, Cw, out, RL, eb0, eb1, r0, rows) ||     // W=512
          try_inverse_fast<32, 32>(c, Cw, out, RL, eb0, eb1, r0, rows) ||    // W=4096
          try_inverse_fast<64, 32>(c, Cw, out, RL, eb0, eb1, r0, rows))) {   // W=8192
-        *carried = out != nullptr;
+        // 1: carried into limbs; 2: decoded into floats (Cw not written)
+        *carried = out ? 1 : c->dec_req ? 2 : 0;
         MFH_HIP(hipGetLastError());
         return MFH_OK;
     }
