@@ -252,8 +252,8 @@ constexpr int XCH_DWORDS = XCH_GROUPS * 16 * XCH_ROW;     // 256 elements: 15 KB
 
 // t: this thread's element among the NE
 template <int MODE, int NE>
-__device__ __forceinline__ void xch_write(uint32_t *buf, const int (&z)[XCH_PLANES / (MODE == MFH_MODE_K7 ? 6 : 3)],
-                                          int t)
+__device__ __forceinline__ void xch_write(
+    uint32_t *buf, const int (&z)[XCH_PLANES / (MODE == MFH_MODE_K7 ? 6 : 3)], int t)
 {
     constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
     constexpr int CPC = XCH_PLANES / PL;
