@@ -194,6 +194,31 @@ def test_generic_kernels_match(gpu, orc, monkeypatch):
             assert np.array_equal(ctx.mm(A, B, RL), want), (n, L)
 
 
+def test_fused_decode_matches_separate_decode(gpu, orc, monkeypatch):
+    """fp32 and fp64 products: the specialised inverse kernels decode each
+    element from their planes in LDS, the generic kernels write the int64
+    planes and decode them in a separate pass; both give the same bits
+    (n = 45: a ragged last workgroup in both)."""
+    n = 45
+    X = orc.fp32_rand(n * n, SEED, -30, 30)
+    Y = orc.fp32_rand(n * n, SEED_B, -30, 30)
+    rng = np.random.default_rng(11)
+    Xd = rng.standard_normal(n * n) * np.exp2(rng.integers(-40, 40, n * n))
+    Yd = rng.standard_normal(n * n) * np.exp2(rng.integers(-40, 40, n * n))
+    res = []
+    for generic in (False, True):
+        if generic:
+            monkeypatch.setenv("MFH_GENERIC_KERNELS", "1")
+        with gpu.Ctx(n, 32) as ctx:
+            f32 = ctx.fpx_mm(X, Y, 256, 256).view(np.uint32)
+        with gpu.Ctx(n, 128) as ctx:
+            f64 = ctx.fpx_mm_f64(Xd, Yd, 1024, 1024).view(np.uint64)
+        res.append((f32, f64))
+    assert np.count_nonzero(res[0][0]) > n * n // 2 and np.count_nonzero(res[0][1]) > n * n // 2
+    assert np.array_equal(res[0][0], res[1][0])
+    assert np.array_equal(res[0][1], res[1][1])
+
+
 def test_device_generator_matches_host(gpu, orc, lib):
     n, L = 96, 32
     with gpu.Ctx(n, L) as ctx:
