@@ -161,6 +161,22 @@ __device__ __forceinline__ long long combine_classes(const int32_t *p, size_t cs
     return v;
 }
 
+// The same from class values already in registers (MODE at compile time)
+template <int MODE>
+__device__ __forceinline__ long long combine_raw(const int *r)
+{
+    if constexpr (MODE == MFH_MODE_K7) {
+        const long long P0 = r[0], P1 = r[1], P2 = r[2], P3 = r[3], P4 = r[4], P5 = r[5];
+        const long long c1 = P3 - P0 - P1, c2 = P4 - P0 - P2 + P1, c3 = P5 - P1 - P2;
+        return P0 + c1 * 128 + c2 * 16384 + c3 * 2097152 + P2 * 268435456;
+    } else {
+        long long v = 0;
+#pragma unroll
+        for (int m = MFH_CLASSES - 1; m >= 0; --m) v = v * 256 + (long long)r[m];
+        return v;
+    }
+}
+
 // Digit planes of one transformed value v (plane stride nnp):
 //  B8: balanced base-2^8 digits, i.e. the low bytes of v, (v + 2^7) >> 8 and
 //      (v + 2^15 + 2^7) >> 16 (each the floor that makes the lower digits
@@ -895,8 +911,12 @@ __device__ __forceinline__ void decode_value(const Plane &plane, int P, int RL, 
 // DEC >= 0 (CARRY false): instead of writing Cw, one thread per element
 // decodes the element's planes from LDS into fp32 / fp64 (MFH_DEC_*) at
 // dec_out with scale 2^-SAB (the semantics of k_decode).
+// PF: the K7 classes of the next point are loaded while the current one is
+// combined (the W = 8192 fused plan: 1.55 -> 1.47 ms at n = 256; equal at
+// W = 2048 and 512).
 template <int NB, int K, bool CARRY, int NPASS = 2,
-          bool NT = !(CARRY && NB == 32 && K == 16), int DEC = -1>
+          bool NT = !(CARRY && NB == 32 && K == 16), int DEC = -1,
+          bool PF = CARRY && NB == 64 && K == 32>
 __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict__ C5,
                                                       int64_t *__restrict__ Cw,
                                                       uint16_t *__restrict__ out, int RL,
@@ -924,6 +944,34 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
         const bool valid = e < eb1;
         const int i = valid ? (int)(e / n) - r0 : 0, jj = valid ? (int)(e % n) : 0;
         long long X[NB];
+        if (PF && mode == MFH_MODE_K7) {
+            // K7 classes of point j + 1 loaded while point j is combined
+            // (an element outside the band reads element 0's and discards
+            // them); the scheduling barriers keep the loads one point ahead
+            const size_t cs = mfh_c5_class_stride(np_, K);
+            const int32_t *p0 = C5 + mfh_c5_index(0, valid ? i : 0, valid ? jj : 0, c, np_, 6, K,
+                                                  rows);
+            const size_t js = mfh_c5_index(1, 0, 0, 0, np_, 6, K, rows);
+            int cur[6], nx[6];
+#pragma unroll
+            for (int m = 0; m < 6; ++m) cur[m] = ld_cls<NT>(p0 + m * cs);
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                if (j + 1 < NB) {
+#pragma unroll
+                    for (int m = 0; m < 6; ++m) nx[m] = ld_cls<NT>(p0 + (j + 1) * js + m * cs);
+                }
+                int r = 0;
+#pragma unroll
+                for (int bit = 1, rb = NB >> 1; bit < NB; bit <<= 1, rb >>= 1)
+                    if (j & bit) r |= rb;
+                const long long v = combine_raw<MFH_MODE_K7>(cur);
+                X[r] = valid ? v : 0;
+#pragma unroll
+                for (int m = 0; m < 6; ++m) cur[m] = nx[m];
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             int r = 0;
@@ -933,6 +981,7 @@ __global__ __launch_bounds__(256) void k_inverse_fast(const int32_t *__restrict_
             X[r] = valid ? combine_classes<NT>(C5 + mfh_c5_index(j, i, jj, c, np_, ncl, K, rows),
                                            mfh_c5_class_stride(np_, K), mode)
                          : 0;
+        }
         }
 #pragma unroll
         for (int len = 2; len <= NB; len <<= 1) {
