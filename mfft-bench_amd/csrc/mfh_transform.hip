@@ -1470,11 +1470,13 @@ bool try_inverse_fast(mfh_ctx *c, int64_t *Cw, uint16_t *&out, int RL, size_t eb
     if (c->NB != NB || c->K != K) return false;
     if (out) return try_inverse_fast_as<NB, K, true, 1>(c, Cw, out, RL, eb0, eb1, r0, rows);
     out = nullptr;
+    // decode fused: one pass of 256/K elements per workgroup, as with the
+    // fused carry (fp32 n=2048: inverse 2.26 -> 1.93 ms against two passes)
     if (c->dec_req == MFH_DEC_F32 + 1)
-        return try_inverse_fast_as<NB, K, false, 2, MFH_DEC_F32>(c, Cw, out, RL, eb0, eb1, r0,
+        return try_inverse_fast_as<NB, K, false, 1, MFH_DEC_F32>(c, Cw, out, RL, eb0, eb1, r0,
                                                                  rows);
     if (c->dec_req == MFH_DEC_F64 + 1)
-        return try_inverse_fast_as<NB, K, false, 2, MFH_DEC_F64>(c, Cw, out, RL, eb0, eb1, r0,
+        return try_inverse_fast_as<NB, K, false, 1, MFH_DEC_F64>(c, Cw, out, RL, eb0, eb1, r0,
                                                                  rows);
     return try_inverse_fast_as<NB, K, false>(c, Cw, out, RL, eb0, eb1, r0, rows);
 }
