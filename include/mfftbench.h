@@ -136,7 +136,12 @@ void mm_mfft_signed(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
                     const mfft_plan *p, kernel_t k, uint16_t *out, int RL);
 
 /* ---- fp32/fp64 fixed-point embedding (src/mfftbench.h:182-199,
- *      src/fpfixed.c) ------------------------------------------------------ */
+ *      src/fpfixed.c) ------------------------------------------------------
+ * fpx_ctx has exactly the reference's fields and layout (72 bytes on
+ * x86-64), so a caller built against either header may own it (on the
+ * stack, as src/mlgemm.c:723 does).  What the fused fpx_mm_f32/_f64 need
+ * beyond it is kept inside the library, keyed by the context's A32 planes,
+ * and released by fpx_free. */
 typedef struct {
     int n, L, sig;
     int SA, SB;
@@ -144,7 +149,6 @@ typedef struct {
     int32_t *A32, *B32;     /* signed limb planes, L*n*n each (host)      */
     int64_t *Cw;            /* exact product, 2L-1 int64 planes (host)    */
     double enc_secs, dec_secs;
-    void *dev;              /* inputs last encoded (fpx_mm_f32/_f64)      */
 } fpx_ctx;
 
 int  fpx_init(fpx_ctx *c, const float *A, const float *B, int n,
@@ -157,12 +161,16 @@ void fpx_decode_ld(fpx_ctx *c, long double *C);                         /* :196 
 void fpx_decode_f32(fpx_ctx *c, float *C);                              /* :197 */
 void fpx_decode_f64(fpx_ctx *c, double *C);                             /* :198 */
 void fpx_free(fpx_ctx *c);                                              /* :199 */
-/* encode -> MFFT product -> decode entirely on the device, from the fp32
- * matrices given to fpx_encode (no reference counterpart; equals
- * conv_mfft + fpx_decode_f32 bit for bit). */
+/* encode -> MFFT product -> decode entirely on the device (no reference
+ * counterpart; equals conv_mfft + fpx_decode_f32 bit for bit).  It
+ * multiplies the matrices of the most recent fpx_encode on this context:
+ * fpx_encode keeps a device copy of A and B for it, so the caller may free
+ * or reuse its A and B as soon as fpx_encode returns.  The copy is
+ * released by fpx_free.  Returns 0, or a negative MFH_E_* code (MFH_E_ARG
+ * when the context has no fp32 encoding). */
 int  fpx_mm_f32(fpx_ctx *c, const mfft_plan *p, float *C);
-/* the same for fp64 matrices given to fpx_encode_d (equals conv_mfft +
- * fpx_decode_f64 bit for bit; no reference counterpart) */
+/* the same for the fp64 matrices of the most recent fpx_encode_d (equals
+ * conv_mfft + fpx_decode_f64 bit for bit; no reference counterpart) */
 int  fpx_mm_f64(fpx_ctx *c, const mfft_plan *p, double *C);
 
 /* Status of the most recent call on this thread: 0, or a negative code

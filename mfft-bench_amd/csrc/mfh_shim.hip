@@ -234,10 +234,17 @@ const char *mfh_device_arch(void)
     return g_arch;
 }
 
-int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
+}  // extern "C"
+
+namespace {
+// Checks (n, L, plan) and fills the shape fields of a zeroed context: sizes,
+// plan, kernel family and whether 6-product digits serve any of its
+// products.  The int64 and int32 bounds must hold for some digit setting of
+// the exact track (a superset of the others'); a size only some settings
+// admit serves the products that use them (MFH_E_BOUND for the others, at
+// call time).
+int shape_init(mfh_ctx *c, int n, int L, const mfh_plan *p)
 {
-    if (!out || !p) return MFH_E_ARG;
-    *out = nullptr;
     if (n < 1 || L < 2 || (L & (L - 1))) return MFH_E_ARG;
     // the flat plan of src/mfft.c:77-95
     if (p->L != L || p->S < 1 || p->NB < 2 || p->K != 2 * p->S ||
@@ -246,41 +253,54 @@ int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
     if (p->K != 4 && p->K != 8 && p->K != 16 && p->K != 32) return MFH_E_UNSUPPORTED;
     // digit range: |a^| <= (NB/2) * 65535 must fit three balanced int8 digits
     if ((long long)(p->NB / 2) * 65535 > MFH_DIGIT_MAX) return MFH_E_BOUND;
-    const int np_ = (n + MFH_KBLK - 1) / MFH_KBLK * MFH_KBLK;
-    // the int64 and int32 bounds hold for some digit setting of the exact
-    // track (a superset of the others'); a size only some settings admit
-    // serves the products that use them (MFH_E_BOUND for the others, at
-    // call time)
+    memset(c, 0, sizeof *c);
+    c->n = n; c->np = (n + MFH_KBLK - 1) / MFH_KBLK * MFH_KBLK;
+    c->L = L; c->S = p->S; c->NB = p->NB; c->K = p->K; c->g = p->g;
+    c->use_fast = getenv("MFH_GENERIC_KERNELS") ? 0 : 1;
+    select_mode(c, MFH_IN_U16);
+    if (!c->mode_ok) return MFH_E_BOUND;
+    bool k7_ok = c->mode == MFH_MODE_K7;
+    select_mode(c, -1);
+    k7_ok |= c->mode_ok && c->mode == MFH_MODE_K7;
+    c->k7_ok = k7_ok;
+    select_mode(c, MFH_IN_U16);
+    return MFH_OK;
+}
+
+// per padded row of A: its digit planes and its class results
+size_t digit_row_bytes(const mfh_ctx *c)
+{
+    return (size_t)c->NB * c->K * (c->k7_ok ? MFH_PLANES_MAX : MFH_DIGITS) * c->np;
+}
+size_t c5_row_bytes(const mfh_ctx *c)
+{
+    return (size_t)c->NB * (c->k7_ok ? MFH_CLASSES_MAX : MFH_CLASSES) * c->K * c->np *
+           sizeof(int32_t);
+}
+}  // namespace
+
+extern "C" {
+
+int mfh_create(mfh_ctx **out, int n, int L, const mfh_plan *p)
+{
+    if (!out || !p) return MFH_E_ARG;
+    *out = nullptr;
     mfh_ctx shape;
-    memset(&shape, 0, sizeof shape);
-    shape.n = n; shape.np = np_; shape.L = L; shape.S = p->S; shape.NB = p->NB; shape.K = p->K;
-    shape.use_fast = getenv("MFH_GENERIC_KERNELS") ? 0 : 1;
-    select_mode(&shape, MFH_IN_U16);
-    if (!shape.mode_ok) return MFH_E_BOUND;
-    bool k7_ok = shape.mode == MFH_MODE_K7;
-    select_mode(&shape, -1);
-    k7_ok |= shape.mode_ok && shape.mode == MFH_MODE_K7;
-    int rc = check_device();
+    int rc = shape_init(&shape, n, L, p);
     if (rc) return rc;
+    if ((rc = check_device())) return rc;
 
     mfh_ctx *c = new mfh_ctx;
-    memset(c, 0, sizeof *c);
-    c->n = n; c->np = np_; c->L = L; c->S = p->S; c->NB = p->NB; c->K = p->K; c->g = p->g;
+    *c = shape;
     c->dev = 0;
-    c->use_fast = shape.use_fast;
     if (hipSetDevice(0) != hipSuccess || hipStreamCreate(&c->stream) != hipSuccess) {
         delete c;
         return MFH_E_HIP;
     }
     for (int k = 0; k < 5; ++k) (void)hipEventCreate(&c->ev[k]);
-    const size_t nnp = (size_t)np_ * np_, nn = (size_t)n * n;
-    c->k7_ok = k7_ok;
-    const int planes = c->k7_ok ? MFH_PLANES_MAX : MFH_DIGITS;
-    const int classes = c->k7_ok ? MFH_CLASSES_MAX : MFH_CLASSES;
-    select_mode(c, MFH_IN_U16);
-    // per padded row of A: its digit planes and its class results
-    const size_t digit_row = (size_t)c->NB * c->K * planes * np_;
-    const size_t c5_row = (size_t)c->NB * classes * c->K * np_ * sizeof(int32_t);
+    const int np_ = c->np;
+    const size_t nn = (size_t)n * n;
+    const size_t digit_row = digit_row_bytes(c), c5_row = c5_row_bytes(c);
     const size_t cw_bytes = (size_t)(2 * L - 1) * nn * sizeof(int64_t);
     const size_t bt_bytes = (size_t)L * nn * sizeof(int32_t);
     rc = band_rows(np_, digit_row + c5_row, digit_row * np_ + cw_bytes + bt_bytes, &c->hb);

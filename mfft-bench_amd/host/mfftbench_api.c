@@ -417,8 +417,54 @@ static void scan_d(const double *X, size_t nn, int *lo, int *hi, int *any)
     *lo = l; *hi = h; *any = seen;
 }
 
-/* the fp inputs given to fpx_encode / fpx_encode_d, for fpx_mm_f32/f64 */
-typedef struct { const void *A, *B; } fpx_src;
+/* What fpx_mm_f32 / fpx_mm_f64 need beyond the reference's fpx_ctx: device
+ * copies of the matrices of the context's most recent encode, and a device
+ * output buffer.  One entry per live context, keyed by its A32 planes
+ * (unique while the context lives; a copied fpx_ctx finds the same entry),
+ * removed by fpx_free.  Guarded by g_lock. */
+typedef struct fpx_keep {
+    const int32_t *key;
+    int f64, n;
+    void *dA, *dB, *dC;
+    struct fpx_keep *next;
+} fpx_keep;
+static fpx_keep *g_keep;
+
+static fpx_keep **keep_find(const int32_t *key)
+{
+    fpx_keep **k = &g_keep;
+    while (*k && (*k)->key != key) k = &(*k)->next;
+    return k;
+}
+
+static void keep_release(fpx_keep *k)
+{
+    if (k->dA) mfh_free(k->dA);
+    if (k->dB) mfh_free(k->dB);
+    if (k->dC) mfh_free(k->dC);
+    free(k);
+}
+
+/* device copies of A and B for the context keyed by `key` (replacing
+ * those of an earlier encode) */
+static int keep_inputs(const int32_t *key, const void *A, const void *B, int n, int f64)
+{
+    const size_t bytes = (size_t)n * n * (f64 ? 8 : 4);
+    fpx_keep *k = calloc(1, sizeof *k);
+    if (!k) return MFH_E_NOMEM;
+    k->key = key; k->f64 = f64; k->n = n;
+    int rc = mfh_malloc(&k->dA, bytes);
+    if (!rc) rc = mfh_malloc(&k->dB, bytes);
+    if (!rc) rc = mfh_h2d(k->dA, A, bytes);
+    if (!rc) rc = mfh_h2d(k->dB, B, bytes);
+    if (rc) { keep_release(k); return rc; }
+    pthread_mutex_lock(&g_lock);
+    fpx_keep **slot = keep_find(key);
+    if (*slot) { fpx_keep *old = *slot; k->next = old->next; keep_release(old); }
+    *slot = k;
+    pthread_mutex_unlock(&g_lock);
+    return MFH_OK;
+}
 
 /* grid and limb count (src/fpfixed.c:59-78): `sig` significand bits, `wr`
  * limbs one shifted significand can touch; then the int64 guard and the host
@@ -478,22 +524,23 @@ int fpx_init_d(fpx_ctx *c, const double *A, const double *B, int n, int force_bi
     return fpx_setup(c, n, loA, hiA, loB, hiB, anyA, anyB, 53, 5, force_bits);
 }
 
-/* limb planes A32/B32 written on the device; the inputs are remembered for
- * fpx_mm_f32 / fpx_mm_f64 */
+/* limb planes A32/B32 written on the device (the reference's encode, timed
+ * into enc_secs as src/fpfixed.c:204 does); then device copies of A and B
+ * are kept for fpx_mm_f32 / fpx_mm_f64 */
 static void encode_common(fpx_ctx *c, const void *A, const void *B, int f64,
                           const char *name)
 {
-    double t0 = now_sec();
     t_last_error = 0;
+    if (!c || !c->A32 || !c->B32 || !A || !B) { fail(name, MFH_E_ARG); return; }
+    double t0 = now_sec();
     int rc = f64 ? mfh_fpx_encode_f64(A, c->n, c->L, c->SA, c->A32)
                  : mfh_fpx_encode(A, c->n, c->L, c->SA, c->A32);
     if (!rc)
         rc = f64 ? mfh_fpx_encode_f64(B, c->n, c->L, c->SB, c->B32)
                  : mfh_fpx_encode(B, c->n, c->L, c->SB, c->B32);
     if (rc) { fail(name, rc); return; }
-    fpx_src *s = c->dev ? (fpx_src *)c->dev : calloc(1, sizeof(fpx_src));
-    if (s) { s->A = A; s->B = B; c->dev = s; }
     c->enc_secs = now_sec() - t0;
+    if ((rc = keep_inputs(c->A32, A, B, c->n, f64))) fail(name, rc);
 }
 
 void fpx_encode(fpx_ctx *c, const float *A, const float *B)
@@ -529,17 +576,24 @@ void fpx_decode_ld(fpx_ctx *c, long double *C)
     if (rc) fail("fpx_decode_ld", rc);
 }
 
+/* the product of the kept device copies, decoded on the device into the
+ * entry's output buffer, then copied to C */
 static int fpx_mm_common(fpx_ctx *c, const mfft_plan *p, void *C, int f64, const char *name)
 {
     t_last_error = 0;
-    fpx_src *s = c ? (fpx_src *)c->dev : NULL;
-    if (!s || !p || !C || (c->sig == 53) != (f64 != 0)) return fail(name, MFH_E_ARG);
+    if (!c || !c->A32 || !p || !C) return fail(name, MFH_E_ARG);
+    const size_t bytes = (size_t)c->n * c->n * (f64 ? 8 : 4);
     pthread_mutex_lock(&g_lock);
+    fpx_keep *k = *keep_find(c->A32);
+    int rc = (!k || k->f64 != (f64 != 0) || k->n != c->n) ? MFH_E_ARG : MFH_OK;
+    if (!rc && !k->dC) rc = mfh_malloc(&k->dC, bytes);
     mfh_ctx *h = NULL;
-    int rc = get_ctx(c->n, c->L, p, &h);
+    if (!rc) rc = get_ctx(c->n, c->L, p, &h);
     if (!rc)
-        rc = f64 ? mfh_fpx_mm_f64(h, s->A, s->B, c->SA, c->SB, C)
-                 : mfh_fpx_mm(h, s->A, s->B, c->SA, c->SB, C);
+        rc = f64 ? mfh_fpx_mm_f64_dev(h, k->dA, k->dB, c->SA, c->SB, k->dC)
+                 : mfh_fpx_mm_dev(h, k->dA, k->dB, c->SA, c->SB, k->dC);
+    if (!rc) rc = mfh_sync(h);
+    if (!rc) rc = mfh_d2h(C, k->dC, bytes);
     pthread_mutex_unlock(&g_lock);
     if (rc) return fail(name, rc);
     return 0;
@@ -555,8 +609,17 @@ int fpx_mm_f64(fpx_ctx *c, const mfft_plan *p, double *C)
     return fpx_mm_common(c, p, C, 1, "fpx_mm_f64");
 }
 
+/* src/fpfixed.c:324-328, plus the device copies kept for the context */
 void fpx_free(fpx_ctx *c)
 {
-    free(c->A32); free(c->B32); free(c->Cw); free(c->dev);
-    c->A32 = NULL; c->B32 = NULL; c->Cw = NULL; c->dev = NULL;
+    if (c->A32) {
+        pthread_mutex_lock(&g_lock);
+        fpx_keep **slot = keep_find(c->A32);
+        fpx_keep *k = *slot;
+        if (k) *slot = k->next;
+        pthread_mutex_unlock(&g_lock);
+        if (k) keep_release(k);
+    }
+    free(c->A32); free(c->B32); free(c->Cw);
+    c->A32 = NULL; c->B32 = NULL; c->Cw = NULL;
 }

@@ -41,12 +41,12 @@ class ProfileT(C.Structure):
 
 
 class FpxCtx(C.Structure):
+    """fpx_ctx (src/mfftbench.h:182-189): the reference's fields, 72 bytes"""
     _fields_ = [("n", C.c_int), ("L", C.c_int), ("sig", C.c_int),
                 ("SA", C.c_int), ("SB", C.c_int),
                 ("spreadA", C.c_int), ("spreadB", C.c_int),
                 ("A32", C.c_void_p), ("B32", C.c_void_p), ("Cw", C.c_void_p),
-                ("enc_secs", C.c_double), ("dec_secs", C.c_double),
-                ("dev", C.c_void_p)]
+                ("enc_secs", C.c_double), ("dec_secs", C.c_double)]
 
 
 def _p(a):
