@@ -54,12 +54,13 @@ int r2_layout(long *v, int cap)
 /* src/main.c:207-208, 111-134: seeded inputs, mm_mfft on the device,
  * bigres_equal against the expected limbs.  Returns 1 when equal, 0 with
  * bad = (i, j, w) of the first mismatch, or a negative error code (the
- * library's, or -100 for a plan or allocation failure). */
+ * library's, -99 when the planner has no plan for L, as the recursive one
+ * has none for L < 4, or -100 for an allocation failure). */
 int r2_mm_mfft(int n, int L, uint64_t seed_a, uint64_t seed_b, int is_signed, int rec,
                const uint16_t *want, int RL, int *bad)
 {
     mfft_plan p;
-    if ((rec ? mfft_plan_init_rec(&p, L, n, 0) : mfft_plan_init(&p, L, 0)) != 0) return -100;
+    if ((rec ? mfft_plan_init_rec(&p, L, n, 0) : mfft_plan_init(&p, L, 0)) != 0) return -99;
     uint16_t *A = bigmat_alloc(n, L), *B = bigmat_alloc(n, L);
     uint16_t *out = malloc((size_t)RL * n * n * sizeof(uint16_t));
     int rc = -100;
