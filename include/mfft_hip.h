@@ -32,7 +32,9 @@ enum {
     MFH_E_BOUND = -4,    /* plan/size would overflow a stated accumulator  */
     MFH_E_RANGE = -5,    /* an input limb lies outside [-65535, 65535]     */
     MFH_E_HIP = -6,      /* HIP runtime error                              */
-    MFH_E_UNSUPPORTED = -7
+    MFH_E_UNSUPPORTED = -7,
+    MFH_E_SCRATCH = -8   /* workspace larger than the fixed no-allocation
+                            scratch (mfh_mm_dev_noalloc)                   */
 };
 
 /* Input forms accepted by the transform (the limb reader). */
@@ -94,6 +96,23 @@ int mfh_conv(mfh_ctx *ctx, const int32_t *A32, const int32_t *B32,
 int mfh_mm_dev(mfh_ctx *ctx, int in_kind, const void *dA, const void *dB,
                void *dOut, int RL);
 int mfh_conv_dev(mfh_ctx *ctx, const void *dA32, const void *dB32, void *dCw);
+
+/* mfh_mm_dev with no device allocation: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  No context: the
+ * workspace is one fixed device array of MFH_NOALLOC_BYTES per device, held
+ * from the library's load until the process ends, and sizes whose workspace
+ * exceeds it return MFH_E_SCRATCH before any kernel runs (n = 64 at 1024-bit
+ * entries fits; n = 128 at 512 bits does not).  Same inputs, output and
+ * checks as mfh_mm_dev, and the same kernels.  `stream` is a hipStream_t
+ * passed as void * (NULL: the null stream); the call is ordered on it and
+ * returns without synchronising.  Every call on a device shares that
+ * device's array and leaves it holding its intermediates: calls that overlap
+ * on one device (from two host threads, or on two streams not ordered
+ * against each other) race. */
+#define MFH_NOALLOC_BYTES (64u << 20)
+int mfh_mm_dev_noalloc(int in_kind, const mfh_plan *plan, int n, int L, const void *dA,
+                       const void *dB, void *dOut, int RL, void *stream);
 
 /* fp32 fixed-point embedding on device (src/fpfixed.c semantics):
  * A, B fp32 n x n; scales 2^SA, 2^SB; product rounded once to fp32. */

@@ -4,7 +4,16 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "mfh_internal.hpp"
+
+// Workspace of mfh_mm_dev_noalloc: one fixed array per device, allocated by
+// the runtime when the library's code object is loaded and held until the
+// process ends.  Host code never uses this name as an address (on the host
+// it is only a stand-in for the symbol): the device address comes from
+// hipGetSymbolAddress, per device (noalloc_scratch below).
+static __device__ __align__(256) unsigned char scratch[MFH_NOALLOC_BYTES];
 
 namespace {
 
@@ -15,7 +24,8 @@ const char *kErr[] = {"ok",
                       "plan or size exceeds a stated accumulator bound",
                       "input limb outside [-65535, 65535]",
                       "HIP runtime error",
-                      "unsupported plan"};
+                      "unsupported plan",
+                      "workspace exceeds the fixed no-allocation scratch"};
 
 char g_arch[64];
 
@@ -357,6 +367,82 @@ int mfh_mm_dev(mfh_ctx *c, int kind, const void *dA, const void *dB, void *dOut,
     c->last_out = 0; c->last_RL = RL; c->last_fused = carried;
     mark(c, 4);
     return MFH_OK;
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kMaxDevices];   // device address of `scratch`, per device
+
+// the device address of the current device's scratch array, looked up once
+// per device with that device current
+int noalloc_scratch(void **out)
+{
+    int dev = 0;
+    MFH_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return MFH_E_UNSUPPORTED;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return MFH_E_HIP;
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return MFH_OK;
+}
+}  // namespace
+
+// The buffers of mfh_create's workspace, for one band of all np rows, laid
+// out in the scratch array at 256-byte boundaries (B's transposed limbs as
+// uint16: only the exact-track product runs here).
+int mfh_mm_dev_noalloc(int kind, const mfh_plan *plan, int n, int L, const void *dA,
+                       const void *dB, void *dOut, int RL, void *stream)
+{
+    if (!plan || !dA || !dB || !dOut || RL < 1) return MFH_E_ARG;
+    if (((uintptr_t)dA | (uintptr_t)dB) % 16) return MFH_E_ARG;
+    if (kind != MFH_IN_U16 && kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
+    mfh_ctx c;
+    int rc = shape_init(&c, n, L, plan);
+    if (rc) return rc;
+    const size_t nn = (size_t)n * n;
+    size_t off = 0;
+    auto take = [&off](size_t bytes) {
+        const size_t at = off;
+        off += (bytes + 255) / 256 * 256;
+        return at;
+    };
+    const size_t oAh = take(digit_row_bytes(&c) * c.np), oBh = take(digit_row_bytes(&c) * c.np);
+    const size_t oC5 = take(c5_row_bytes(&c) * c.np);
+    const size_t oCw = take((size_t)(2 * L - 1) * nn * sizeof(int64_t));
+    const size_t oBt = take((size_t)L * nn * sizeof(uint16_t));
+    const size_t oFlag = take(sizeof(int));
+    const bool sums = k7_recode_plan(&c);
+    const size_t oRow = sums ? take((size_t)L * n * sizeof(int64_t)) : 0;
+    const size_t oCol = sums ? take((size_t)L * n * sizeof(int64_t)) : 0;
+    if (off > (size_t)MFH_NOALLOC_BYTES) return MFH_E_SCRATCH;
+    if ((rc = check_device())) return rc;
+    void *base = nullptr;
+    if ((rc = noalloc_scratch(&base))) return rc;
+    unsigned char *b = (unsigned char *)base;
+    c.dAh = (int8_t *)(b + oAh);
+    c.dBh = (int8_t *)(b + oBh);
+    c.dC5 = (int32_t *)(b + oC5);
+    c.dCw = (int64_t *)(b + oCw);
+    c.dBt = b + oBt;
+    c.dFlag = (int *)(b + oFlag);
+    if (sums) {
+        c.dRow = (int64_t *)(b + oRow);
+        c.dCol = (int64_t *)(b + oCol);
+    }
+    c.hb = c.np;
+    c.nbands = 1;
+    c.stream = (hipStream_t)stream;
+    select_mode(&c, kind);
+    int carried = 0;
+    rc = run_conv(&c, kind, dA, dB, c.dCw, 0, 0, (uint16_t *)dOut, RL, &carried);
+    if (rc) return rc;
+    if (!carried) rc = mfh_launch_carry(&c, c.dCw, (uint16_t *)dOut, RL);
+    return rc;
 }
 
 // products that return the caller's own limb convolution (conv_mfft, the

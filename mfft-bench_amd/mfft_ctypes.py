@@ -15,7 +15,8 @@ LIB_PATH = os.path.join(HERE, "lib", "libmfft_hip.so")
 KERNEL_IKJ, KERNEL_PACKED, KERNEL_HIP = 0, 2, 12
 MFH_IN_U16, MFH_IN_U16_SIGNED, MFH_IN_I32 = 0, 1, 2
 ERRORS = {0: "MFH_OK", -1: "MFH_E_NODEV", -2: "MFH_E_NOMEM", -3: "MFH_E_ARG",
-          -4: "MFH_E_BOUND", -5: "MFH_E_RANGE", -6: "MFH_E_HIP", -7: "MFH_E_UNSUPPORTED"}
+          -4: "MFH_E_BOUND", -5: "MFH_E_RANGE", -6: "MFH_E_HIP", -7: "MFH_E_UNSUPPORTED",
+          -8: "MFH_E_SCRATCH"}
 
 
 class MfftError(RuntimeError):
@@ -73,6 +74,7 @@ def load(path=None):
         "mfh_workspace_bytes": ([vp], sz), "mfh_band_rows": ([vp], i),
         "mfh_mm": ([vp, i, vp, vp, vp, i], i), "mfh_conv": ([vp, vp, vp, vp], i),
         "mfh_mm_dev": ([vp, i, vp, vp, vp, i], i), "mfh_conv_dev": ([vp, vp, vp, vp], i),
+        "mfh_mm_dev_noalloc": ([i, pl, i, i, vp, vp, vp, i, vp], i),
         "mfh_fpx_mm_dev": ([vp, vp, vp, i, i, vp], i), "mfh_fpx_mm": ([vp, vp, vp, i, i, vp], i),
         "mfh_fpx_decode_dev": ([vp, vp, i, vp], i),
         "mfh_normalize": ([vp, i, i, vp, i], i), "mfh_fpx_encode": ([vp, i, i, i, vp], i),
