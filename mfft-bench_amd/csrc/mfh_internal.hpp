@@ -106,11 +106,34 @@ static inline bool mfh_class_bound_ok(int K, int np_, int pairs)
 // np / MFH_BANDS_MAX rows)
 #define MFH_BANDS_MAX 64
 
+// Pointwise algorithm.  MFH_PW_FLAT: the K^2 products of each ring product
+// (src/mfft.c:383-395).  MFH_PW_GAUSS: one Karatsuba level on the ring axis
+// in Gauss's three-product form.  With u = y^(K/2) (u^2 = -1) and
+// X = X0 + u X1 (X0, X1 of degree < H = K/2),
+//     A B = (k1 - k3) + u (k1 + k2),
+//     k1 = (A0 + A1) B0,  k2 = A0 (B1 - B0),  k3 = A1 (B0 + B1),
+// three linear convolutions of length H (3 H^2 products instead of 4 H^2).
+// The forward transform writes 3H operand slots per point: A's as
+// [A0 + A1 | A0 | A1], B's as [B0 | B1 - B0 | -(B0 + B1)], so sub-product g
+// multiplies slots gH .. gH+H-1 of both.  Every slot value obeys the bound
+// of a single coefficient: block b contributes one limb to coefficient c
+// and none to c + H or the other way round (its upper H coefficients are
+// zero before the shift y^e), so X[c] +- X[c+H] is still a signed sum of
+// one limb per non-zero block.
+#define MFH_PW_FLAT 0
+#define MFH_PW_GAUSS 1
+// operand slots per evaluation point
+static inline int mfh_slots(int K, int pw) { return pw == MFH_PW_GAUSS ? 3 * K / 2 : K; }
+
 struct mfh_ctx {
     int n, np;            // matrix size, padded to a multiple of 64
     int L, S, NB, K, g;
     int dev;
     int use_fast;         // compile-time specialised kernels when available
+    int pw;               // MFH_PW_GAUSS when the workspace holds Gauss slots
+                          // (fixed at creation), else MFH_PW_FLAT
+    int pwr;              // the current product's algorithm: Gauss needs pw and
+                          // the 6-product digits (set with the digit mode)
     hipStream_t stream;
     // workspace
     int mode;             // digit mode of the current product (MFH_MODE_*)
@@ -123,8 +146,8 @@ struct mfh_ctx {
     int mode_ok;          // the selected digit setting keeps every bound
     int hb;               // row band height: A's digit planes and the class
                           // results hold hb padded rows at a time
-    int8_t *dAh;          // A's digit planes [NB][K][planes][hb][np]
-    int8_t *dBh;          // B's digit planes [NB][K][planes][np][np]
+    int8_t *dAh;          // A's digit planes [NB][slots][planes][hb][np]
+    int8_t *dBh;          // B's digit planes [NB][slots][planes][np][np]
     int32_t *dC5;         // pointwise class results of a band (mfh_c5_index)
     int64_t *dCw;         // coefficient planes [2L-1][n][n]
     void *dBt;            // transposed B input, up to L*n*n int32
@@ -159,10 +182,13 @@ int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
 // with all of B, and the inverse of the band's elements (rows r0.. below n,
 // written at their places in the n x n outputs).  rows is a multiple of 64,
 // or reaches np.
+// side: 0 for A, 1 for B (the operand slots differ under MFH_PW_GAUSS)
 int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
-                       int scale_S, int r0, int rows);
+                       int scale_S, int r0, int rows, int side);
 int mfh_launch_check_i32(mfh_ctx *c, const int32_t *src, int planes);
 int mfh_launch_pointwise(mfh_ctx *c, int rows);
+// ring sizes K with a Gauss pointwise kernel
+bool mfh_gauss_supported(int K);
 // out != nullptr asks for the carry into RL uint16 limbs to be fused;
 // *carried tells whether it was (else Cw holds the coefficient planes)
 int mfh_launch_inverse(mfh_ctx *c, int64_t *Cw, uint16_t *out, int RL, int *carried, int r0,

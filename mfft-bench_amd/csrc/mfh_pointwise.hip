@@ -657,10 +657,378 @@ int launch_cfg(mfh_ctx *c, int rows)
     return MFH_OK;
 }
 
+// ============================================================================
+// Gauss pointwise (MFH_PW_GAUSS, mfh_internal.hpp).  At point j the ring
+// product is Re + u Im with u = y^H, H = K/2, Re = k1 - k3, Im = k1 + k2:
+// three linear convolutions of length H over the operand slots the forward
+// transform wrote, sub-product g multiplying A slots gH .. gH+H-1 with B
+// slots gH .. gH+H-1 (B's carry the signs of Re = k1 + A1 (-(B0+B1))).
+// Folded by u^2 = -1, diagonal s of Re lands on C[s], and diagonal s of Im
+// on C[s+H] (s < H) or, negated, on C[s-H] (s >= H).  A wave owns one
+// 16 x 16 output block and accumulates
+//   g = 2 (A1 x -(B0+B1), Re):  diagonal s into C[s]
+//   g = 1 (A0 x (B1-B0), Im):   diagonal s < H into C[s+H], s >= H into
+//                               ng[s-H] (subtracted at the end of the class)
+//   g = 0 (A0+A1 x B0, both):   diagonal s into a temporary T, then
+//                               C[s] += T and C[s+H] += T or C[s-H] -= T
+// so that every term enters with a fixed sign.  Each accumulator sums at
+// most K digit products per k (C[t], t < H-1: t+9 <= 2H-1), as a flat class
+// accumulator does, so the flat kernel's int32 bound covers them; C is then
+// stored like the flat kernel's class results and the inverse transform is
+// the same.
+//
+// Sub-rounds: (digit pair, 64-wide k block, g), H fragments of A (WBI row
+// blocks) and of B (WBJ column blocks) each.  A round is the three
+// sub-rounds g = 0, 1, 2 of one (pair, k block), and sub-round g always
+// lives in LDS slot g (distinct arrays, so the compiler can tell a copy into
+// one slot from reads of another).  A wave reads its fragment pairs D ahead
+// of the MFMAs that need them, in diagonal order (c1 + c2 = s, two
+// diagonals interleaved so that no MFMA waits on the one before it); after
+// the diagonal group BAR, when every read of the sub-round is done, it waits
+// for its copies of the next sub-round, a barrier follows, and the copies of
+// the same g of the next round go into this slot: they have two
+// sub-rounds to land.  After the group PRE (>= BAR: the next slot is
+// complete by then), the wave reads the first D pairs of the next
+// sub-round, so that its first MFMAs do not wait for LDS.
+// ============================================================================
+template <int K_, int WBI_, int WBJ_, int WPE_, int D_, int BAR_, int PRE_, bool SPLIT_ = false>
+struct GsCfg {
+    static constexpr int K = K_, H = K_ / 2, WBI = WBI_, WBJ = WBJ_, WPE = WPE_;
+    static constexpr int D = D_, BAR = BAR_, PRE = PRE_;
+    static constexpr bool SPLIT = SPLIT_;
+    static constexpr int WAVES = WBI * WBJ, THREADS = WAVES * 64;
+    static constexpr int BI = 16 * WBI, BJ = 16 * WBJ;
+    static constexpr int A_CHUNKS = H * WBI * 64, B_CHUNKS = H * WBJ * 64;   // one sub-round
+    static constexpr int NA = H * WBI / WAVES, NBF = H * WBJ / WAVES;        // copies per wave
+    static constexpr int NPW = NA + NBF;
+    static constexpr int ND = 2 * H - 1;             // diagonals of a length-H convolution
+    // the diagonal group (even s0) in which pair H-1 is read
+    static constexpr int LAST_READ = D >= H ? -1 : ((H - 1 - D) / 2) * 2;
+    static_assert((H * WBI) % WAVES == 0 && (H * WBJ) % WAVES == 0 && WAVES % WBI == 0 &&
+                      WAVES % WBJ == 0,
+                  "copies split evenly over waves");
+    static_assert(D >= 2 && D <= H, "diagonals 0 and 1 need pairs 0 and 1");
+    static_assert(BAR % 2 == 0 && BAR > LAST_READ && BAR < ND, "barrier after the last read");
+    static_assert(PRE % 2 == 0 && PRE >= BAR && PRE < ND, "prefetch after the barrier");
+    static_assert(!SPLIT || PRE > BAR, "split barrier: arrive before waiting");
+    static_assert(NPW < 16, "vmcnt immediate");
+    static_assert(3 * (A_CHUNKS + B_CHUNKS) * 16 <= 160 * 1024, "three slots fit in LDS");
+};
+
+// s_waitcnt vmcnt(V) lgkmcnt(0) (expcnt left alone)
+template <int V>
+__device__ __forceinline__ void vm_lgkm_wait()
+{
+    static_assert(V >= 0 && V < 16, "4-bit vmcnt field");
+    __builtin_amdgcn_s_waitcnt((V & 15) | (7 << 4) | (0 << 8));
+}
+// the same, then a workgroup barrier
+template <int V>
+__device__ __forceinline__ void vm_lgkm_barrier()
+{
+    vm_lgkm_wait<V>();
+    __builtin_amdgcn_s_barrier();
+}
+// Split barrier in LDS (gfx950 has no split s_barrier): a wave arrives by
+// adding 1 to the counter once its own waits are done, goes on with work
+// that needs no other wave, and waits only where it does, until every wave
+// of the workgroup has arrived as often as it has (the counter is never
+// reset; waves arrive in the same sequence).
+// The counter is touched by inline asm: the compiler cannot tell it apart
+// from the LDS slots that copies are still filling and would wait for every
+// copy before each access.  An LDS operation it does not count only makes
+// its own (in-order) lgkmcnt waits stricter.
+__device__ __forceinline__ void split_arrive(int *ctr)
+{
+    const uint32_t a = (uint32_t)(uintptr_t)ctr, one = 1;
+    if ((threadIdx.x & 63) == 0) asm volatile("ds_add_u32 %0, %1" ::"v"(a), "v"(one) : "memory");
+}
+__device__ __forceinline__ void split_wait(int *ctr, int target)
+{
+    const uint32_t a = (uint32_t)(uintptr_t)ctr;
+    for (;;) {
+        int v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+        if (__builtin_amdgcn_readfirstlane(v) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// One sub-round of one wave: the length-H linear convolution of its H A and
+// H B fragments (la, lb: fragment of slot-coefficient 0, strides WBI*64 and
+// WBJ*64 chunks) into acc / ng as G says.  pa / pb hold its first D pairs
+// on entry and the next sub-round's (nla, nlb) on return.  hook(s0) runs
+// after the MFMAs of each diagonal group.
+template <class Cfg, int G, class Hook>
+__device__ __forceinline__ void gs_sub(v4i (&acc)[Cfg::K], v4i (&ng)[Cfg::H - 1],
+                                       v4i (&pa)[Cfg::D], v4i (&pb)[Cfg::D],
+                                       const v4i *__restrict__ la, const v4i *__restrict__ lb,
+                                       const v4i *__restrict__ nla, const v4i *__restrict__ nlb,
+                                       const Hook &hook)
+{
+    constexpr int H = Cfg::H, D = Cfg::D, ND = Cfg::ND;
+    constexpr int SA = Cfg::WBI * 64, SB = Cfg::WBJ * 64;
+    v4i af[H], bf[H];
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+        af[c] = pa[c];
+        bf[c] = pb[c];
+    }
+    v4i tp[2];        // g = 0: the previous group's diagonal sums, folded one group late
+    // g = 0: diagonal s's sum into C[s] and C[s+H] or -C[s-H]
+    auto fold = [&](int s, const v4i &t) {
+        acc[s] += t;
+        if (s < H) acc[s + H] += t;
+        else acc[s - H] -= t;
+    };
+#pragma unroll
+    for (int s0 = 0; s0 < ND; s0 += 2) {
+#pragma unroll
+        for (int c = s0 + D; c < s0 + D + 2; ++c)
+            if (c < H) {
+                af[c] = la[c * SA];
+                bf[c] = lb[c * SB];
+            }
+        v4i t[2];
+#pragma unroll
+        for (int q = 0; q < H; ++q) {
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                const int s = s0 + d;
+                const int lo = s - H + 1 > 0 ? s - H + 1 : 0;
+                const int hi = s < H - 1 ? s : H - 1;
+                const int c1 = lo + q;
+                if (s < ND && c1 <= hi) {
+                    const int c2 = s - c1;
+                    if constexpr (G == 0) {
+                        const v4i z = {0, 0, 0, 0};
+                        t[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[c1], bf[c2],
+                                                                     q == 0 ? z : t[d], 0, 0, 0);
+                    } else if constexpr (G == 1) {
+                        if (s < H)
+                            acc[s + H] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                                af[c1], bf[c2], acc[s + H], 0, 0, 0);
+                        else
+                            ng[s - H] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[c1], bf[c2],
+                                                                              ng[s - H], 0, 0, 0);
+                    } else {
+                        acc[s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[c1], bf[c2], acc[s], 0,
+                                                                       0, 0);
+                    }
+                }
+            }
+        }
+        if constexpr (G == 0) {
+            if (s0 >= 2) {
+                fold(s0 - 2, tp[0]);
+                fold(s0 - 1, tp[1]);
+            }
+            tp[0] = t[0];
+            tp[1] = t[1];
+        }
+        hook(s0);
+        if (s0 == Cfg::PRE) {
+#pragma unroll
+            for (int c = 0; c < D; ++c) {
+                pa[c] = nla[c * SA];
+                pb[c] = nlb[c * SB];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (G == 0) fold(ND - 1, tp[0]);   // the last group holds diagonal ND-1 only
+}
+
+template <class Cfg, int MODE>
+__global__ void __attribute__((amdgpu_flat_work_group_size(Cfg::THREADS, Cfg::THREADS),
+                               amdgpu_waves_per_eu(Cfg::WPE, Cfg::WPE)))
+k_pointwise_gauss(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
+                  int32_t *__restrict__ C5, int np_, int rows, int tiles_j)
+{
+    constexpr int K = Cfg::K, H = Cfg::H, WBI = Cfg::WBI, WBJ = Cfg::WBJ, W = Cfg::WAVES;
+    constexpr int NA = Cfg::NA, NBF = Cfg::NBF, NPW = Cfg::NPW;
+    constexpr int NCLASS = MODE == MFH_MODE_K7 ? 6 : 2 * MFH_DIGITS - 1;
+    constexpr int PL = MODE == MFH_MODE_K7 ? 6 : MFH_DIGITS;     // planes per slot
+    constexpr int NSL = 3 * H;                                    // slots per point
+    __shared__ v4i sA0[Cfg::A_CHUNKS], sA1[Cfg::A_CHUNKS], sA2[Cfg::A_CHUNKS];
+    __shared__ v4i sB0[Cfg::B_CHUNKS], sB1[Cfg::B_CHUNKS], sB2[Cfg::B_CHUNKS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wbi = wave / WBJ, wbj = wave % WBJ;
+    int ti, tj, jp;
+    tile_of(tiles_j, ti, tj, jp);
+    const int i0 = ti * Cfg::BI, j0 = tj * Cfg::BJ;
+    const size_t plane = (size_t)np_ * np_;           // B: all np rows
+    const size_t planeA = (size_t)rows * np_;         // A: the band's rows
+    const int8_t *Aj = Ah + (size_t)jp * NSL * PL * planeA;
+    const int8_t *Bj = Bh + (size_t)jp * NSL * PL * plane;
+    // copies: fragment f = wave + W i of a sub-round is A slot-coefficient
+    // f / WBI at row block f % WBI (= wave % WBI), B likewise with WBJ; a
+    // fragment is 1 KB contiguous in the tiled planes, lane l's 16 bytes at
+    // row l % 16, k 16 (l / 16)
+    const int8_t *a_blk = Aj + (size_t)(wave / WBI) * PL * planeA +
+                          mfh_tile_off(i0 + (wave % WBI) * 16, 0, np_) + (lane & 15) * 64 +
+                          (lane >> 4) * 16;
+    const int8_t *b_blk = Bj + (size_t)(wave / WBJ) * PL * plane +
+                          mfh_tile_off(j0 + (wave % WBJ) * 16, 0, np_) + (lane & 15) * 64 +
+                          (lane >> 4) * 16;
+    const size_t da = (size_t)(W / WBI) * PL * planeA;
+    const size_t db = (size_t)(W / WBJ) * PL * plane;
+    const int kblocks = np_ / MFH_KBLK;
+    const int col = j0 + wbj * 16 + (lane & 15);
+    const int row0 = i0 + wbi * 16 + 4 * (lane >> 4);
+
+    // copies of sub-round g of round rd of class m into slot g
+    auto copy = [&](auto gtag, int m, int rd) {
+        constexpr int G = decltype(gtag)::value;
+        v4i *dA = G == 0 ? sA0 : G == 1 ? sA1 : sA2;
+        v4i *dB = G == 0 ? sB0 : G == 1 ? sB1 : sB2;
+        int rlo, npr;
+        class_pairs<MODE>(m, rlo, npr);
+        const int r = rlo + rd / kblocks, kb = rd % kblocks;
+        const int s = MODE == MFH_MODE_K7 ? r : m - r;
+        const int8_t *a0 = a_blk + ((size_t)G * H * PL + r) * planeA + kb * 1024;
+        const int8_t *b0 = b_blk + ((size_t)G * H * PL + s) * plane + kb * 1024;
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(a0 + i * da),
+                                             (void *)(dA + (wave + i * W) * 64), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NBF; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(b0 + i * db),
+                                             (void *)(dB + (wave + i * W) * 64), 16, 0, 0);
+    };
+    using G0 = std::integral_constant<int, 0>;
+    using G1 = std::integral_constant<int, 1>;
+    using G2 = std::integral_constant<int, 2>;
+    auto rounds_of = [&](int m) {
+        int rlo, npr;
+        class_pairs<MODE>(m, rlo, npr);
+        return npr * kblocks;
+    };
+
+    // arrivals of the split barrier (Cfg::SPLIT)
+    __shared__ int arrived;
+    if (threadIdx.x == 0) arrived = 0;
+    // prologue: the three sub-rounds of round 0 of class 0
+    copy(G0{}, 0, 0);
+    copy(G1{}, 0, 0);
+    copy(G2{}, 0, 0);
+    vm_lgkm_barrier<2 * NPW>();
+    int u = 0;                 // sub-rounds begun
+
+    v4i acc[K], ng[H - 1];
+    constexpr int D = Cfg::D;
+    v4i pa[D], pb[D];          // the first pairs of the next sub-round
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+        pa[c] = sA0[(c * WBI + wbi) * 64 + lane];
+        pb[c] = sB0[(c * WBJ + wbj) * 64 + lane];
+    }
+    // Round (m, rd) runs; (nm, nrd) is the round whose copies this one
+    // issues: the next round, or the last round itself again (the slot is
+    // done with and never read again), so that every sub-round issues
+    // exactly NPW copies and the outstanding copies are known on every path.
+    auto sub = [&](auto gtag, int nm, int nrd) {
+        constexpr int G = decltype(gtag)::value;
+        const v4i *la = (G == 0 ? sA0 : G == 1 ? sA1 : sA2) + wbi * 64 + lane;
+        const v4i *lb = (G == 0 ? sB0 : G == 1 ? sB1 : sB2) + wbj * 64 + lane;
+        const v4i *nla = (G == 0 ? sA1 : G == 1 ? sA2 : sA0) + wbi * 64 + lane;
+        const v4i *nlb = (G == 0 ? sB1 : G == 1 ? sB2 : sB0) + wbj * 64 + lane;
+        gs_sub<Cfg, G>(acc, ng, pa, pb, la, lb, nla, nlb, [&](int s0) {
+            if constexpr (Cfg::SPLIT) {
+                // arrive once this wave's copies of the next sub-round have
+                // landed and its reads of this slot are done; before copying
+                // into the slot and reading the next one, wait until every
+                // wave has
+                if (s0 == Cfg::BAR) {
+                    vm_lgkm_wait<NPW>();
+                    split_arrive(&arrived);
+                } else if (s0 == Cfg::PRE) {
+                    split_wait(&arrived, Cfg::WAVES * (u + 1));
+                    copy(gtag, nm, nrd);
+                }
+            } else if (s0 == Cfg::BAR) {
+                // this wave's copies of the next sub-round have landed (only
+                // those of the one after it may still be in flight) and its
+                // reads of this slot are done; after the barrier every
+                // wave's are
+                vm_lgkm_barrier<NPW>();
+                copy(gtag, nm, nrd);
+            }
+        });
+        ++u;
+    };
+#pragma unroll 1
+    for (int m = 0; m < NCLASS; ++m) {
+#pragma unroll
+        for (int t = 0; t < K; ++t) acc[t] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < H - 1; ++t) ng[t] = v4i{0, 0, 0, 0};
+        const int rounds = rounds_of(m);
+#pragma unroll 1
+        for (int rd = 0; rd < rounds; ++rd) {
+            int nm = rd + 1 < rounds ? m : m + 1, nrd = rd + 1 < rounds ? rd + 1 : 0;
+            if (nm == NCLASS) {
+                nm = m;
+                nrd = rd;
+            }
+            sub(G0{}, nm, nrd);
+            sub(G1{}, nm, nrd);
+            sub(G2{}, nm, nrd);
+        }
+#pragma unroll
+        for (int t = 0; t < H - 1; ++t) acc[t] -= ng[t];
+        // store this class: rows 4*(lane/16)+v, column lane%16, K values of t
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+#pragma unroll
+            for (int tt = 0; tt < K; tt += 4) {
+                const v4i qv = {acc[tt][v], acc[tt + 1][v], acc[tt + 2][v], acc[tt + 3][v]};
+                __builtin_nontemporal_store(
+                    qv, (v4i *)(C5 + mfh_c5_index(jp, row0 + v, col, tt, np_, NCLASS, K, rows) +
+                                (size_t)m * mfh_c5_class_stride(np_, K)));
+            }
+        }
+    }
+    // the last round's copies into LDS complete before the workgroup ends
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));
+}
+
+template <class Cfg>
+int launch_gauss(mfh_ctx *c, int rows)
+{
+    if (c->np % MFH_KBLK || rows % Cfg::BI || c->np % Cfg::BJ || rows < 1 || rows > c->np)
+        return MFH_E_UNSUPPORTED;
+    const int tiles_i = rows / Cfg::BI, tiles_j = c->np / Cfg::BJ;
+    dim3 grid((unsigned)(tiles_i * tiles_j), (unsigned)c->NB);
+    if (c->mode == MFH_MODE_K7)
+        hipLaunchKernelGGL((k_pointwise_gauss<Cfg, MFH_MODE_K7>), grid, dim3(Cfg::THREADS), 0,
+                           c->stream, c->dAh, c->dBh, c->dC5, c->np, rows, tiles_j);
+    else
+        hipLaunchKernelGGL((k_pointwise_gauss<Cfg, MFH_MODE_B8>), grid, dim3(Cfg::THREADS), 0,
+                           c->stream, c->dAh, c->dBh, c->dC5, c->np, rows, tiles_j);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
 }  // namespace
+
+// K values with a Gauss kernel (the forward transform writes Gauss slots
+// only for these)
+bool mfh_gauss_supported(int K) { return K == 16; }
 
 int mfh_launch_pointwise(mfh_ctx *c, int rows)
 {
+    if (c->pw == MFH_PW_GAUSS) {
+        switch (c->K) {
+        // 64 x 32 tiles, 8 waves at 2 per SIMD, pairs read 4 ahead, barrier
+        // after diagonal group 4, the next sub-round's first pairs read
+        // after group 8
+        case 16: return launch_gauss<GsCfg<16, 4, 2, 2, 4, 4, 8, true>>(c, rows);
+        default: return MFH_E_UNSUPPORTED;
+        }
+    }
     switch (c->K) {
     case 4:  return launch_cfg<PwCfg<4, 4, 2, 2>>(c, rows);
     // K = 8 and K = 16: copy fills with the B fragments held in registers,

@@ -119,12 +119,15 @@ void select_mode(mfh_ctx *c, int kind)
     };
     c->mode = MFH_MODE_B8;
     c->recode = c->offset = c->mode_ok = 0;
+    c->pwr = MFH_PW_FLAT;
     for (const auto &k : cand)
         if (k.ok) {
             c->mode = k.mode;
             c->recode = k.recode;
             c->offset = k.offset;
             c->mode_ok = 1;
+            // the Gauss kernels take the 6-product digits
+            c->pwr = c->pw == MFH_PW_GAUSS && k.mode == MFH_MODE_K7 ? MFH_PW_GAUSS : MFH_PW_FLAT;
             return;
         }
 }
@@ -163,12 +166,12 @@ int run_conv(mfh_ctx *c, int kind, const void *dA, const void *dB, int64_t *Cw,
                                          c->stream)))
             return rc;
     }
-    if ((rc = mfh_launch_forward(c, kind, c->dBt, c->dBh, SB, 0, c->np))) return rc;
+    if ((rc = mfh_launch_forward(c, kind, c->dBt, c->dBh, SB, 0, c->np, 1))) return rc;
     int fused = 0, b = 0;
     for (int r0 = 0; r0 < c->n; r0 += c->hb, ++b) {
         const int rows = c->hb < c->np - r0 ? c->hb : c->np - r0;
         mark_band(c, b, 0);
-        if ((rc = mfh_launch_forward(c, kind, dA, c->dAh, SA, r0, rows))) return rc;
+        if ((rc = mfh_launch_forward(c, kind, dA, c->dAh, SA, r0, rows, 0))) return rc;
         mark_band(c, b, 1);
         if ((rc = mfh_launch_pointwise(c, rows))) return rc;
         mark_band(c, b, 2);
@@ -267,6 +270,11 @@ int shape_init(mfh_ctx *c, int n, int L, const mfh_plan *p)
     c->n = n; c->np = (n + MFH_KBLK - 1) / MFH_KBLK * MFH_KBLK;
     c->L = L; c->S = p->S; c->NB = p->NB; c->K = p->K; c->g = p->g;
     c->use_fast = getenv("MFH_GENERIC_KERNELS") ? 0 : 1;
+    // the Gauss pointwise where a kernel exists for K (MFH_POINTWISE=flat:
+    // the K^2-product kernel throughout)
+    const char *pwe = getenv("MFH_POINTWISE");
+    c->pw = mfh_gauss_supported(c->K) && !(pwe && strcmp(pwe, "flat") == 0) ? MFH_PW_GAUSS
+                                                                             : MFH_PW_FLAT;
     select_mode(c, MFH_IN_U16);
     if (!c->mode_ok) return MFH_E_BOUND;
     bool k7_ok = c->mode == MFH_MODE_K7;
@@ -280,7 +288,8 @@ int shape_init(mfh_ctx *c, int n, int L, const mfh_plan *p)
 // per padded row of A: its digit planes and its class results
 size_t digit_row_bytes(const mfh_ctx *c)
 {
-    return (size_t)c->NB * c->K * (c->k7_ok ? MFH_PLANES_MAX : MFH_DIGITS) * c->np;
+    return (size_t)c->NB * mfh_slots(c->K, c->pw) * (c->k7_ok ? MFH_PLANES_MAX : MFH_DIGITS) *
+           c->np;
 }
 size_t c5_row_bytes(const mfh_ctx *c)
 {
@@ -665,8 +674,11 @@ int mfh_work(const mfh_ctx *c, double *ops, double *fwd, double *inv)
     const double nnp = (double)c->np * c->np, nn = (double)c->n * c->n;
     const double pts = (double)c->NB * c->K;
     const double products = c->mode == MFH_MODE_K7 ? 6.0 : 9.0;
-    if (ops) *ops = 2.0 * products * c->NB * (double)c->K * c->K * nnp * c->np;
-    if (fwd) *fwd = 2.0 * ((double)c->L * nn * 2.0 + pts * mfh_planes(c->mode) * nnp);
+    // ring products issued per point: K^2, or 3 (K/2)^2 with the Gauss split
+    const double ring = c->pwr == MFH_PW_GAUSS ? 0.75 * c->K * c->K : (double)c->K * c->K;
+    const double slots = (double)c->NB * mfh_slots(c->K, c->pwr);
+    if (ops) *ops = 2.0 * products * c->NB * ring * nnp * c->np;
+    if (fwd) *fwd = 2.0 * ((double)c->L * nn * 2.0 + slots * mfh_planes(c->mode) * nnp);
     if (inv) {
         // class results in; then the int64 coefficient planes (written, and
         // read back by the carry or decode) unless the carry ran inside the

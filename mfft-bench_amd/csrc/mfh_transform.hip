@@ -226,6 +226,32 @@ __device__ __forceinline__ void digit_vals(int v, int *d)
     }
 }
 
+// Operand slot sl of a point whose K ring coefficients are z.  GS = 0: the
+// coefficients themselves (K slots).  GS = 1 (operand A) / 2 (operand B):
+// the 3H Gauss slots of MFH_PW_GAUSS (mfh_internal.hpp), H = K/2:
+//   A: [z0 + z1 | z0 | z1],  B: [z0 | z1 - z0 | -(z0 + z1)]
+// with z0 = z[0..H), z1 = z[H..K).
+template <int GS, int K>
+__device__ __forceinline__ int slot_val(const int *z, int sl)
+{
+    if constexpr (GS == 0) {
+        return z[sl];
+    } else {
+        constexpr int H = K / 2;
+        const int g = sl / H, c = sl % H;
+        if constexpr (GS == 1) return g == 0 ? z[c] + z[c + H] : g == 1 ? z[c] : z[c + H];
+        else return g == 0 ? z[c] : g == 1 ? z[c + H] - z[c] : -z[c] - z[c + H];
+    }
+}
+// the same with the ring size and slot kind known at run time
+__device__ __forceinline__ int slot_val_rt(const int *z, int sl, int K, int gs)
+{
+    if (gs == 0) return z[sl];
+    const int H = K / 2, g = sl / H, c = sl % H;
+    if (gs == 1) return g == 0 ? z[c] + z[c + H] : g == 1 ? z[c] : z[c + H];
+    return g == 0 ? z[c] : g == 1 ? z[c + H] - z[c] : -z[c] - z[c + H];
+}
+
 // low bytes of a, b, c, d as one dword (a lowest)
 __device__ __forceinline__ uint32_t pack4_lo(int a, int b, int c, int d)
 {
@@ -321,10 +347,12 @@ __device__ __forceinline__ void xch_store(const uint32_t *buf, int8_t *o, size_t
 // (j, c, r) holds digit r of X[j][c] as a rows x np int8 matrix in 16 x 64
 // tiles (mfh_tile_off; the whole operand when row0 = 0, rows = np; the other
 // forward kernels take the same band and layout).
+// gs: operand slots as slot_val_rt (0: the K coefficients; 1, 2: the 3K/2
+// Gauss slots of operand A, B).
 template <class Src, int MODE>
 __global__ __launch_bounds__(256) void k_forward_generic(
     Src src, int8_t *__restrict__ out, int np_, int LS, int S, int NB, int K,
-    int g, int row0, int rows)
+    int g, int row0, int rows, int gs)
 {
     const size_t nnp = (size_t)rows * np_;         // the band's elements (plane stride)
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -332,8 +360,10 @@ __global__ __launch_bounds__(256) void k_forward_generic(
     const int i = row0 + (int)(e / np_), k = (int)(e % np_);
     const bool valid = i < src.n && k < src.n;
     const size_t toff = mfh_tile_off(i - row0, k, np_);
-    const int twoK = 2 * K;
+    const int twoK = 2 * K, nsl = gs ? 3 * K / 2 : K;
+    constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
     for (int j = 0; j < NB; ++j) {
+        int z[32];
         for (int c = 0; c < K; ++c) {
             int acc = 0;
             if (valid) {
@@ -345,9 +375,11 @@ __global__ __launch_bounds__(256) void k_forward_generic(
                     else if (s >= K && s < K + S) acc -= src.get(b * S + s - K, i, k);
                 }
             }
-            constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
-            store_digits<MODE>(out + ((size_t)(j * K + c) * PL) * nnp + toff, nnp, acc);
+            z[c] = acc;
         }
+        for (int sl = 0; sl < nsl; ++sl)
+            store_digits<MODE>(out + ((size_t)(j * nsl + sl) * PL) * nnp + toff, nnp,
+                               slot_val_rt(z, sl, K, gs));
     }
 }
 
@@ -360,7 +392,7 @@ __global__ __launch_bounds__(256) void k_forward_generic(
 template <class Src, int MODE>
 __global__ __launch_bounds__(256) void k_forward_window(Src src, int8_t *__restrict__ out,
                                                         int np_, int S, int NB, int K, int g,
-                                                        int row0, int rows)
+                                                        int row0, int rows, int gs)
 {
     constexpr int NW = Src::NW;
     const size_t nnp = (size_t)rows * np_;
@@ -378,18 +410,22 @@ __global__ __launch_bounds__(256) void k_forward_window(Src src, int8_t *__restr
         b[t] = u / S;
         s[t] = u % S;
     }
-    const int twoK = 2 * K;
+    const int twoK = 2 * K, nsl = gs ? 3 * K / 2 : K;
+    constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
     for (int j = 0; j < NB; ++j) {
         int p[NW];
 #pragma unroll
         for (int t = 0; t < NW; ++t) p[t] = (s[t] + (g * j * b[t]) % twoK) % twoK;
+        int z[32];
         for (int c = 0; c < K; ++c) {
             int acc = 0;
 #pragma unroll
             for (int t = 0; t < NW; ++t) acc += p[t] == c ? r[t] : p[t] == c + K ? -r[t] : 0;
-            constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
-            store_digits<MODE>(out + ((size_t)(j * K + c) * PL) * nnp + toff, nnp, acc);
+            z[c] = acc;
         }
+        for (int sl = 0; sl < nsl; ++sl)
+            store_digits<MODE>(out + ((size_t)(j * nsl + sl) * PL) * nnp + toff, nnp,
+                               slot_val_rt(z, sl, K, gs));
     }
 }
 
@@ -475,12 +511,15 @@ __device__ __forceinline__ void load_limbs(LimbsI32<L> &x, const Src &src, int i
 // XCH_DWORDS at xb (256 elements per workgroup, one thread each); XB = 3:
 // staged per wave (64 elements per workgroup, wave w's buffer at
 // xb + w * XCH_DWORDS / 4).
-template <int S, int NB, int Q, int q, int MODE, class Limbs, int XB = 0>
+// GS: the operand slots written per point (slot_val: 0 the K coefficients,
+// 1 / 2 the 3K/2 Gauss slots of operand A / B).
+template <int S, int NB, int Q, int q, int MODE, class Limbs, int XB = 0, int GS = 0>
 __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t nnp,
                                               uint32_t *xb = nullptr)
 {
     constexpr int PL = MODE == MFH_MODE_K7 ? 6 : 3;
     constexpr int K = 2 * S, P = NB / Q, LS = NB / 2;
+    constexpr int NSL = GS ? 3 * K / 2 : K;
     constexpr int g = 2 * K / NB, twoK = 2 * K;
     int z[P][K];
 #pragma unroll
@@ -533,27 +572,28 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
         const int j = q + Q * jp;
         if constexpr (XB == 0) {
 #pragma unroll
-            for (int c = 0; c < K; ++c)
-                store_digits<MODE>(o + (size_t)((j * K + c) * PL) * nnp, nnp, z[pos][c]);
+            for (int sl = 0; sl < NSL; ++sl)
+                store_digits<MODE>(o + (size_t)((j * NSL + sl) * PL) * nnp, nnp,
+                                   slot_val<GS, K>(z[pos], sl));
         } else if constexpr (XB == 3) {
             // the wave's own buffer: LDS operations of one wave complete in
             // order; the memory clobbers keep the compiler from moving the
             // other lanes' reads above the writes, or the next chunk's writes
             // above this chunk's reads
             constexpr int CPC = XCH_PLANES / PL;
-            static_assert(K % CPC == 0, "whole chunks per point");
+            static_assert(NSL % CPC == 0, "whole chunks per point");
             const int lane = threadIdx.x & 63;
             uint32_t *buf = xb + (threadIdx.x >> 6) * (XCH_DWORDS / 4);
             int8_t *wg = o - lane;
 #pragma unroll
-            for (int c0 = 0; c0 < K; c0 += CPC) {
+            for (int c0 = 0; c0 < NSL; c0 += CPC) {
                 int zc[CPC];
 #pragma unroll
-                for (int c = 0; c < CPC; ++c) zc[c] = z[pos][c0 + c];
+                for (int c = 0; c < CPC; ++c) zc[c] = slot_val<GS, K>(z[pos], c0 + c);
                 asm volatile("" ::: "memory");
                 xch_write<MODE, 64>(buf, zc, lane);
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                xch_store<64>(buf, wg + (size_t)((j * K + c0) * PL) * nnp, nnp, lane);
+                xch_store<64>(buf, wg + (size_t)((j * NSL + c0) * PL) * nnp, nnp, lane);
             }
         } else {
             // chunks of CPC coefficients; chunk k of the kernel uses buffer
@@ -562,19 +602,19 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
             // barrier before the reads of chunk k also orders every read of
             // chunk k-1 before the writes of chunk k+1 into its buffer.
             constexpr int CPC = XCH_PLANES / PL;
-            static_assert(K % CPC == 0, "whole chunks per point");
+            static_assert(NSL % CPC == 0, "whole chunks per point");
             int8_t *wg = o - threadIdx.x;
 #pragma unroll
-            for (int c0 = 0; c0 < K; c0 += CPC) {
-                const int k = (q * P + pos) * (K / CPC) + c0 / CPC;
+            for (int c0 = 0; c0 < NSL; c0 += CPC) {
+                const int k = (q * P + pos) * (NSL / CPC) + c0 / CPC;
                 uint32_t *buf = xb + (k % XB) * XCH_DWORDS;
                 int zc[CPC];
 #pragma unroll
-                for (int c = 0; c < CPC; ++c) zc[c] = z[pos][c0 + c];
+                for (int c = 0; c < CPC; ++c) zc[c] = slot_val<GS, K>(z[pos], c0 + c);
                 if (XB == 1 && k > 0) __syncthreads();
                 xch_write<MODE, 256>(buf, zc, threadIdx.x);
                 __syncthreads();
-                xch_store<256>(buf, wg + (size_t)((j * K + c0) * PL) * nnp, nnp, threadIdx.x);
+                xch_store<256>(buf, wg + (size_t)((j * NSL + c0) * PL) * nnp, nnp, threadIdx.x);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -583,27 +623,28 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
 
 // Threads of part p (p = thread / E, wave-uniform) produce the output
 // classes q = p, p + TPE, ... of their element.
-template <int S, int NB, int Q, int MODE, int TPE, int PART, class Limbs, int XB, int... is>
+template <int S, int NB, int Q, int MODE, int TPE, int PART, class Limbs, int XB, int GS,
+          int... is>
 __device__ __forceinline__ void forward_part(const Limbs &x, int8_t *o, size_t nnp, uint32_t *xb,
                                              std::integer_sequence<int, is...>)
 {
     // scheduling barriers between classes (and after each point's stores,
     // in forward_class): left free, the scheduler interleaves classes and
     // the S = 16 kernels need 256+ registers (140 with the barriers)
-    ((forward_class<S, NB, Q, PART + TPE * is, MODE, Limbs, XB>(x, o, nnp, xb),
+    ((forward_class<S, NB, Q, PART + TPE * is, MODE, Limbs, XB, GS>(x, o, nnp, xb),
       __builtin_amdgcn_sched_barrier(0)),
      ...);
 }
-template <int S, int NB, int Q, int MODE, int TPE, class Limbs, int XB, int PART = 0>
+template <int S, int NB, int Q, int MODE, int TPE, class Limbs, int XB, int GS, int PART = 0>
 __device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *o, size_t nnp,
                                               uint32_t *xb)
 {
     if constexpr (PART < TPE) {
         if (part == PART)
-            forward_part<S, NB, Q, MODE, TPE, PART, Limbs, XB>(
+            forward_part<S, NB, Q, MODE, TPE, PART, Limbs, XB, GS>(
                 x, o, nnp, xb, std::make_integer_sequence<int, Q / TPE>{});
         else
-            forward_parts<S, NB, Q, MODE, TPE, Limbs, XB, PART + 1>(part, x, o, nnp, xb);
+            forward_parts<S, NB, Q, MODE, TPE, Limbs, XB, GS, PART + 1>(part, x, o, nnp, xb);
     }
 }
 
@@ -618,7 +659,7 @@ __device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *
 // band's element count must be a multiple of 256, so every thread of every
 // workgroup has an element and reaches every barrier).
 template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src, int E = 256,
-          int XB = 0>
+          int XB = 0, int GS = 0>
 __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restrict__ out, int np_,
                                                       int top_mode, int row0, int rows)
 {
@@ -692,7 +733,7 @@ __global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restric
         const bool valid = i < src.n && k < src.n;
         load_limbs<L>(x, src, i, k, valid);
     }
-    forward_parts<S, NB, Q, MODE, TPE, Limbs, XB>(part, x, out + e, nnp, xbuf);
+    forward_parts<S, NB, Q, MODE, TPE, Limbs, XB, GS>(part, x, out + e, nnp, xbuf);
 }
 
 // |limb| <= 65535 for int32 inputs (the transform and digit bounds assume it)
@@ -1300,17 +1341,35 @@ int mfh_launch_transpose(const void *src, void *dst, int planes, int n,
 namespace {
 // compile-time plans: (S, NB) with Q output classes of length NB/Q
 template <int S, int NB, int MODE, bool RECODE, class Src, class Limbs, int E = 256,
-          int Q = NB / 4, int XB = 0>
-bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_mode, int row0, int rows)
+          int Q = NB / 4, int XB = 0, int GS = 0>
+bool try_fast1(mfh_ctx *c, const Src &s, int8_t *dst, int top_mode, int row0, int rows)
 {
     if (c->S != S || c->NB != NB || c->mode != MODE || (c->recode != 0) != RECODE) return false;
     if (top_mode == 2 && !RECODE) return false;
     const size_t nnp = (size_t)rows * c->np;
     if (XB > 0 && nnp % E) return false;     // staged stores need whole workgroups
-    hipLaunchKernelGGL((k_forward_fast<S, NB, Q, MODE, RECODE, Limbs, Src, E, XB>),
+    hipLaunchKernelGGL((k_forward_fast<S, NB, Q, MODE, RECODE, Limbs, Src, E, XB, GS>),
                        dim3((unsigned)((nnp + E - 1) / E)), dim3(256), 0, c->stream, s, dst,
                        c->np, top_mode, row0, rows);
     return true;
+}
+// gs: operand slots (slot_val); Gauss slots are compiled for the rings with
+// a Gauss pointwise kernel, in the 6-product digit mode only
+template <int S, int NB, int MODE, bool RECODE, class Src, class Limbs, int E = 256,
+          int Q = NB / 4, int XB = 0>
+bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_mode, int row0, int rows, int gs)
+{
+    if (gs == 0)
+        return try_fast1<S, NB, MODE, RECODE, Src, Limbs, E, Q, XB, 0>(c, s, dst, top_mode,
+                                                                         row0, rows);
+    if constexpr (MODE == MFH_MODE_K7 && 2 * S == 16) {
+        if (gs == 1)
+            return try_fast1<S, NB, MODE, RECODE, Src, Limbs, E, Q, XB, 1>(c, s, dst, top_mode,
+                                                                             row0, rows);
+        return try_fast1<S, NB, MODE, RECODE, Src, Limbs, E, Q, XB, 2>(c, s, dst, top_mode,
+                                                                         row0, rows);
+    }
+    return false;
 }
 
 // Plans with 256 elements per workgroup store their digits through LDS
@@ -1318,7 +1377,8 @@ bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_mode, int row0, int
 // transpose), 9.7 -> 6.2 ms at W = 512 and n = 4096, 1.71 -> 1.1 ms for
 // fp32 at n = 2048; two buffers (one barrier per chunk) measured equal or
 // slower.
-bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, int rows)
+bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, int rows,
+                      int gs)
 {
     constexpr int K7 = MFH_MODE_K7, B8 = MFH_MODE_B8;
     if (c->n % 8) return false;   // staged 16-byte loads need rows of 8k limbs
@@ -1326,61 +1386,64 @@ bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, 
     // classes of 4; 214 VGPRs, within the two waves per SIMD the LDS allows):
     // forward stage 2-3 % faster; 16 classes of 2 were 5 % slower
     return try_fast<8, 32, K7, true, SrcU16, LimbsLds<128>, 256, 4, 1>(c, s, dst, ts, r0,
-                                                                       rows) ||  // W=2048
-           try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>, 256, 8, 1>(c, s, dst, ts, r0, rows) ||
+                                                                       rows, gs) ||  // W=2048
+           try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>, 256, 8, 1>(c, s, dst, ts, r0, rows,
+                                                                       gs) ||
            try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>, 256, 4, 1>(c, s, dst, ts, r0,
-                                                                       rows) ||  // W=1024
+                                                                       rows, gs) ||  // W=1024
            try_fast<16, 64, K7, true, SrcU16, LimbsLds<512, 64>, 64, 32, 3>(c, s, dst, ts, r0,
-                                                                           rows) ||  // W=8192
+                                                                           rows, gs) ||  // W=8192
            try_fast<16, 64, B8, false, SrcU16, LimbsLds<512, 64>, 64, 32, 3>(c, s, dst, ts, r0,
-                                                                            rows) ||
+                                                                            rows, gs) ||
            try_fast<4, 16, K7, false, SrcU16, LimbsLds<32>, 256, 4, 1>(c, s, dst, ts, r0,
-                                                                       rows) ||  // W=512
+                                                                       rows, gs) ||  // W=512
            try_fast<16, 32, K7, false, SrcU16, LimbsLds<256, 64>, 64, 16, 3>(c, s, dst, ts, r0,
-                                                                            rows);  // W=4096
+                                                                            rows, gs);  // W=4096
 }
 }  // namespace
 
 template <class Src>
-void launch_generic(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid, int LS, int r0, int rows)
+void launch_generic(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid, int LS, int r0, int rows,
+                    int gs)
 {
     if (c->mode == MFH_MODE_K7)
         hipLaunchKernelGGL((k_forward_generic<Src, MFH_MODE_K7>), grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g, r0, rows);
+                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g, r0, rows, gs);
     else
         hipLaunchKernelGGL((k_forward_generic<Src, MFH_MODE_B8>), grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g, r0, rows);
+                           s, dst, c->np, LS, c->S, c->NB, c->K, c->g, r0, rows, gs);
 }
 
 template <class Src>
-void launch_window(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid, int r0, int rows)
+void launch_window(mfh_ctx *c, const Src &s, int8_t *dst, dim3 grid, int r0, int rows, int gs)
 {
     if (c->mode == MFH_MODE_K7)
         hipLaunchKernelGGL((k_forward_window<Src, MFH_MODE_K7>), grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, c->S, c->NB, c->K, c->g, r0, rows);
+                           s, dst, c->np, c->S, c->NB, c->K, c->g, r0, rows, gs);
     else
         hipLaunchKernelGGL((k_forward_window<Src, MFH_MODE_B8>), grid, dim3(256), 0, c->stream,
-                           s, dst, c->np, c->S, c->NB, c->K, c->g, r0, rows);
+                           s, dst, c->np, c->S, c->NB, c->K, c->g, r0, rows, gs);
 }
 
 int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
-                       int scale_S, int r0, int rows)
+                       int scale_S, int r0, int rows, int side)
 {
     const size_t nnp = (size_t)rows * c->np;
     const size_t nn = (size_t)c->n * c->n;
     dim3 grid((unsigned)((nnp + 255) / 256));
     const int LS = c->L / c->S;
+    const int gs = c->pwr == MFH_PW_GAUSS ? 1 + side : 0;
     if (c->use_fast) {
         bool done = false;
         if (in_kind == MFH_IN_U16 || in_kind == MFH_IN_U16_SIGNED ||
             in_kind == MFH_IN_U16_OFFSET) {
             SrcU16 s{(const uint16_t *)src, nn, c->n, c->L};
             const int top = in_kind == MFH_IN_U16 ? 0 : in_kind == MFH_IN_U16_SIGNED ? 1 : 2;
-            done = forward_fast_u16(c, s, dst, top, r0, rows);
+            done = forward_fast_u16(c, s, dst, top, r0, rows, gs);
         } else if (in_kind == MFH_IN_F32) {
             SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
             done = try_fast<4, 16, MFH_MODE_K7, false, SrcF32, LimbsI32<32>, 256, 4, 1>(
-                c, s, dst, 0, r0, rows);
+                c, s, dst, 0, r0, rows, gs);
         }
         if (done) {
             MFH_HIP(hipGetLastError());
@@ -1390,27 +1453,27 @@ int mfh_launch_forward(mfh_ctx *c, int in_kind, const void *src, int8_t *dst,
     switch (in_kind) {
     case MFH_IN_U16: {
         SrcU16 s{(const uint16_t *)src, nn, c->n, c->L};
-        launch_generic<SrcU16>(c, s, dst, grid, LS, r0, rows);
+        launch_generic<SrcU16>(c, s, dst, grid, LS, r0, rows, gs);
         break;
     }
     case MFH_IN_U16_SIGNED: {
         SrcU16Signed s{(const uint16_t *)src, nn, c->n, c->L};
-        launch_generic<SrcU16Signed>(c, s, dst, grid, LS, r0, rows);
+        launch_generic<SrcU16Signed>(c, s, dst, grid, LS, r0, rows, gs);
         break;
     }
     case MFH_IN_I32: {
         SrcI32 s{(const int32_t *)src, nn, c->n, c->L};
-        launch_generic<SrcI32>(c, s, dst, grid, LS, r0, rows);
+        launch_generic<SrcI32>(c, s, dst, grid, LS, r0, rows, gs);
         break;
     }
     case MFH_IN_F32: {
         SrcF32 s{(const float *)src, nn, c->n, c->L, scale_S};
-        launch_window<SrcF32>(c, s, dst, grid, r0, rows);
+        launch_window<SrcF32>(c, s, dst, grid, r0, rows, gs);
         break;
     }
     case MFH_IN_F64: {
         SrcF64 s{(const double *)src, nn, c->n, c->L, scale_S};
-        launch_window<SrcF64>(c, s, dst, grid, r0, rows);
+        launch_window<SrcF64>(c, s, dst, grid, r0, rows, gs);
         break;
     }
     case MFH_IN_U16_OFFSET:
