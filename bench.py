@@ -98,24 +98,63 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def host_cpu():
+    """(CPU model, usable cores) of this host"""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 0
+    return model, cores
+
+
 def cpu_baseline(n, L, nprod_total):
     """Reference CPU path (oracle/_ref: the reference's own C sources,
-    packed leaf) on a bounded sample, 1 thread.  Pointwise: `s` of the
-    NB*K^2 leaf products timed at full n and scaled.  Transform, pack, fold
-    and normalize: the reference's own phase profile of a whole mm_mfft at
-    n/8 with the same plan, scaled by 64 (those phases are O(n^2))."""
+    packed leaf), 1 thread.  When a whole mm_mfft fits in about 10 s (the
+    1024-bit n=64 workload: ~0.2 s) it is timed whole, best of 3.  Otherwise
+    a bounded sample: `s` of the NB*K^2 leaf products timed at full n and
+    scaled, plus the reference's own phase profile (transform, pack, fold,
+    normalize) of a whole mm_mfft at n/8 with the same plan, scaled by 64
+    (those phases are O(n^2))."""
     from oracle_ctypes import load_reference
     import numpy as np
     ref = load_reference()
     kind = "reference"
     if ref is None:
         return None
+    model, ncores = host_cpu()
     lib = ref.lib
+    rp = ref.plan(L)
     A = np.random.default_rng(1).integers(0, 1 << 16, size=n * n).astype(np.int32)
     B = np.random.default_rng(2).integers(0, 1 << 16, size=n * n).astype(np.int32)
+    Cacc = np.zeros(n * n, dtype=np.int64)
+    t0 = time.perf_counter()
+    ref.mm_accum(Cacc, A, B, n, 1, ref.KERNEL_PACKED)
+    est = (time.perf_counter() - t0) * nprod_total
+    base = {"unit": "ms", "cores": 1, "kind": kind, "cpu_model": model, "host_cores": ncores}
+    if est < 10.0:
+        As = ref.bigmat_rand(n, L, 12345)
+        Bs = ref.bigmat_rand(n, L, 12345 ^ 0xABCDEF)
+        best = None
+        for _ in range(3):
+            t0 = time.perf_counter()
+            ref.mm_mfft(As, Bs, n, L, rp, 2 * L + 1)
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        return dict(base, value=round(best * 1e3, 3),
+                    sample=(f"reference src/ built from source, packed leaf, 1 thread: whole "
+                            f"mm_mfft at n={n}, L={L} on the seeded inputs, best of 3 "
+                            f"(not extrapolated)"))
     # transformed values at these plans are at most ~21 bits; the leaf's cost
     # does not depend on the values.  Time leaf products until ~10 s of work.
-    Cacc = np.zeros(n * n, dtype=np.int64)
     times = []
     while sum(times) < 10.0 and len(times) < 1024:
         t0 = time.perf_counter()
@@ -136,7 +175,6 @@ def cpu_baseline(n, L, nprod_total):
     prof_on.value = 1
     As = ref.bigmat_rand(ns, L, 12345)
     Bs = ref.bigmat_rand(ns, L, 12345 ^ 0xABCDEF)
-    rp = ref.plan(L)
     t0 = time.perf_counter()
     ref.mm_mfft(As, Bs, ns, L, rp, 2 * L + 1)
     wall = time.perf_counter() - t0
@@ -144,30 +182,35 @@ def cpu_baseline(n, L, nprod_total):
     rest_small = wall - prof.pointwise   # widen, pack, build_ops, transforms, fold, normalize
     scale = (n / ns) ** 2
     total_s = nprod_total * t_leaf + rest_small * scale
-    return {
-        "value": round(total_s * 1e3, 1), "unit": "ms", "cores": 1, "kind": kind,
-        "sample": (f"reference src/ built from source, packed leaf, 1 thread: {s} of "
-                   f"{nprod_total} n={n} leaf products timed (median {t_leaf:.3f} s each) "
-                   f"x {nprod_total}; other phases from the reference's own profile of one "
-                   f"mm_mfft at n={ns} ({rest_small:.3f} s) x {scale:.0f}; extrapolated"),
-    }
+    return dict(base, value=round(total_s * 1e3, 1),
+                sample=(f"reference src/ built from source, packed leaf, 1 thread: {s} of "
+                        f"{nprod_total} n={n} leaf products timed (median {t_leaf:.3f} s each) "
+                        f"x {nprod_total}; other phases from the reference's own profile of one "
+                        f"mm_mfft at n={ns} ({rest_small:.3f} s) x {scale:.0f}; extrapolated"))
 
 
 def method_table(args):
     """The reference bench's result table (src/main.c:137-165) for the device
     methods on one exact-track workload: the schoolbook (limbplane, the
     speedup baseline as in src/main.c:293-297), the flat MFFT plan and the
-    recursive plan.  `products` is each method's n x n product count as the
-    reference defines it; `kernel_calls` is the reference's count of leaf
-    mm_accum calls, which the device methods do not make (0); `exact`
-    compares every limb with the schoolbook's result and checks it by
-    Freivalds' test."""
-    import numpy as np
-    import mfft_ctypes as M
+    recursive plan (and, at K = 16, the flat plan with the K^2-product
+    pointwise kernel forced).  `products` is each method's n x n product
+    count as the reference defines it (mfft_plan.nprod); `issued` is the
+    ring products the device issued (NB times the per-point count of
+    mfh_pointwise_info; each is 6 or 9 int8 digit GEMMs); `kernel_calls` is
+    the reference's count of leaf mm_accum calls, which the device methods do
+    not make (0); `exact` compares every limb with the schoolbook's result
+    and checks it by Freivalds' test."""
     n, W, ekind = CONFIGS[args.config]
     if ekind == "fp32":
         log("bench.py --table: exact-track workloads only (c1, c2, c3, c5)")
         sys.exit(2)
+    return method_table_for(n, W, ekind, args)
+
+
+def method_table_for(n, W, ekind, args, header=True):
+    import numpy as np
+    import mfft_ctypes as M
     signed = ekind == "signed"
     L = W // 16
     RL = 2 * L + 1
@@ -194,37 +237,53 @@ def method_table(args):
     secs = timed(lambda: M.check(lib.mfh_limbplane_mm_dev(None, kind, dA.ptr, dB.ptr, n, L,
                                                           dCw.ptr, dRef.ptr, RL)), 2)
     ref_out = dRef.download(np.uint16, RL * n * n)
-    rows.append(["limbplane", "hip", L * L, 0, secs, ref_out])
-    for name, p in (("mfft", M.plan(L)), ("mfft-rec", M.plan_rec(L, n))):
+    rows.append(["limbplane", "hip", L * L, L * L, 0, secs, ref_out])
+    variants = [("mfft", M.plan(L), False), ("mfft-rec", M.plan_rec(L, n), False)]
+    if M.plan(L) is not None and M.plan(L).K == 16:
+        # the K^2-product kernel beside the default Gauss one at this ring
+        variants.insert(1, ("mfft-flatpw", M.plan(L), True))
+    for name, p, flat in variants:
         if p is None:
             continue
-        ctx = M.Ctx(n, L, p)
+        if flat:
+            os.environ["MFH_POINTWISE"] = "flat"
+        try:
+            ctx = M.Ctx(n, L, p)
+        except M.MfftError as e:
+            # outside the stated bounds (MFH_E_BOUND) or ring sizes: no row
+            log(f"[table] {name} n={n} W={W}: {e}")
+            continue
+        finally:
+            os.environ.pop("MFH_POINTWISE", None)
         secs = timed(lambda: M.check(lib.mfh_mm_dev(ctx.h, kind, dA.ptr, dB.ptr, dO.ptr, RL)),
                      max(1, args.steps))
         ctx.sync()
         out = dO.download(np.uint16, RL * n * n)
-        rows.append([name, "hip", p.nprod, 0, secs, out])
+        ring, _ = ctx.pointwise_info()
+        rows.append([name, "hip", p.nprod, p.NB * ring, 0, secs, out])
         ctx.close()
     A = host_rand_u16(n, L, 12345)
     B = host_rand_u16(n, L, 12345 ^ 0xABCDEF)
-    base = rows[0][4]
+    base = rows[0][5]
     for r in rows:
-        out = r[5]
+        out = r[6]
         ok = freivalds_check(A, B, out, n, L, RL, signed)
         ok = ok and bool(np.array_equal(out, ref_out))
-        r[5] = ok
+        r[6] = ok
     if args.csv:
-        print("method,kernel,products,kernel_calls,seconds,speedup,exact")
-        for name, k, prod, calls, secs, ok in rows:
-            print(f"{name},{k},{prod},{calls},{secs:.6f},{(base / secs if base else 0.0):.3f},"
-                  f"{'yes' if ok else 'NO'}")
+        if header:
+            print("n,bits,method,kernel,products,issued,kernel_calls,seconds,speedup,exact")
+        for name, k, prod, issued, calls, secs, ok in rows:
+            print(f"{n},{W},{name},{k},{prod},{issued},{calls},{secs:.6f},"
+                  f"{(base / secs if base else 0.0):.3f},{'yes' if ok else 'NO'}")
     else:
         print(f"n={n} W={W} ({ekind}) on {lib.mfh_device_arch().decode()}")
-        print(f"\n{'method':<14} {'kernel':<9} {'n*n products':>12} {'seconds':>10} {'speedup':>9}  exact")
-        print("-" * 73)
-        for name, k, prod, calls, secs, ok in rows:
-            print(f"{name:<14} {k:<9} {prod:>12} {secs:>10.4f} {(base / secs if base else 0.0):>8.2f}x"
-                  f"  {'yes' if ok else 'NO!'}")
+        print(f"\n{'method':<14} {'kernel':<9} {'n*n products':>12} {'issued':>8} "
+              f"{'seconds':>10} {'speedup':>9}  exact")
+        print("-" * 82)
+        for name, k, prod, issued, calls, secs, ok in rows:
+            print(f"{name:<14} {k:<9} {prod:>12} {issued:>8} {secs:>10.4f} "
+                  f"{(base / secs if base else 0.0):>8.2f}x  {'yes' if ok else 'NO!'}")
     for b in (dA, dB, dRef, dO, dCw):
         b.free()
 
@@ -238,7 +297,8 @@ def main():
     ap.add_argument("--n", type=int, default=0,
                     help="with --bits: an exact-track workload of this size instead of --config "
                          "(the reference bench's --n / --bits, src/main.c:333-366)")
-    ap.add_argument("--bits", type=int, default=0, help="entry width W (a power of two >= 32)")
+    ap.add_argument("--bits", "--width", type=int, default=0,
+                    help="entry width W (a power of two >= 32)")
     ap.add_argument("--signed", action="store_true",
                     help="with --n/--bits: two's complement entries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -252,6 +312,12 @@ def main():
                     help="instead of the JSON line: the reference bench's method table "
                          "(src/main.c:137-165) for the device methods on this workload")
     ap.add_argument("--csv", action="store_true", help="the same table as CSV")
+    ap.add_argument("--sweep-width", "--sweep", action="store_true",
+                    help="the method table at widths 128, 256, .., 8192 bits for --n "
+                         "(default 64), as src/main.c:384-386")
+    ap.add_argument("--sweep-n", action="store_true",
+                    help="the method table at n = 32, 64, .. up to --n (default 64) for "
+                         "--width (default 256), as src/main.c:387-389")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -279,6 +345,22 @@ def main():
             f"{2 * nbytes / dt / 1e9:.1f} GB/s read+write")
         src.free()
         dst.free()
+        return
+
+    if args.sweep_width or args.sweep_n:
+        ekind = "signed" if args.signed else "unsigned"
+        nmax = args.n or 64
+        W = args.bits or 256
+        if nmax < 1 or W < 32 or W & (W - 1):
+            log("bench.py: sweeps need --n >= 1 and --width a power of two >= 32")
+            sys.exit(2)
+        cases = ([(nmax, b) for b in (128, 256, 512, 1024, 2048, 4096, 8192)]
+                 if args.sweep_width else
+                 [(m, W) for m in (32 << i for i in range(16)) if m <= nmax])
+        for i, (m, b) in enumerate(cases):
+            if i and not args.csv:
+                print()
+            method_table_for(m, b, ekind, args, header=(i == 0))
         return
 
     if args.n or args.bits:
@@ -338,9 +420,16 @@ def main():
     ctx.set_timing(False)
     ms = elapsed * 1e3 / args.steps
     st = stage / args.steps
+    # int8 ops the pointwise kernel issued (over the np = 64-padded size: n
+    # here is a multiple of 64 unless --n says otherwise), and the minimum
+    # HBM bytes of the forward and inverse stages
     ops, fwd_b, inv_b = ctx.work()
     inv_bytes = inv_b          # inverse + fold + carry/decode, as the library ran them
+    ring_pp, digit_pp = ctx.pointwise_info()
     nprod = p.NB * p.K * p.K
+    # the effective rate on the 9-digit-product basis BASELINE.md defines
+    # (9 NB K^2 2 n^3 int8 ops per product, whatever the kernels issue)
+    ops9 = 9.0 * nprod * 2.0 * float(n) ** 3
     tops_issued = ops / (ms * 1e-3) / 1e12
     tops_pw = ops / (st[1] * 1e-3) / 1e12
     log(f"[bench] ms/product {ms:.3f}  stages(ms) fwd {st[0]:.3f} pw {st[1]:.3f} "
@@ -388,7 +477,15 @@ def main():
                                f", plan S={p.S} NB={p.NB} K={p.K}, seeds 12345/12345^0xABCDEF",
                    "n": n, "width_bits": W, "limbs": L, "S": p.S, "NB": p.NB, "K": p.K,
                    "parallelism": "single GPU"},
-        "int8_tops_effective": round(tops_issued, 1),
+        "int8_tops_effective": round(ops9 / (ms * 1e-3) / 1e12, 1),
+        "int8_tops_issued": round(tops_issued, 1),
+        "int8_tops_basis": (f"effective: 9*NB*K^2*2n^3 = {ops9:.4g} int8 ops per product (9 "
+                            f"digit products per ring product, K^2 ring products per point); "
+                            f"issued: {ops:.4g} int8 ops the pointwise kernel ran ({digit_pp} "
+                            f"digit products x {ring_pp} ring products per point)"),
+        "pointwise": {"ring_products_per_point": ring_pp, "digit_products": digit_pp,
+                      "algorithm": ("Gauss split of the ring halves (3 (K/2)^2)"
+                                    if ring_pp != p.K * p.K else "K^2 ring products")},
         "mfma_pct_pointwise": round(100.0 * tops_pw / INT8_PEAK_TOPS, 2),
         "decomposition_independent_tops": round(nprod * 2.0 * n ** 3 / (ms * 1e-3) / 1e12, 2),
         "stage_ms": {"forward": round(st[0], 3), "pointwise": round(st[1], 3),
@@ -397,8 +494,10 @@ def main():
                     "inverse_fold_carry": round(inv_bytes / ((st[2] + st[3]) * 1e-3) / 1e9, 1)},
         "verified": verified,
         "roofline": {"bound": "mfma", "achieved": round(tops_pw, 1), "peak": INT8_PEAK_TOPS,
-                     "unit": "TFLOP/s", "frac": round(tops_pw / INT8_PEAK_TOPS, 4),
-                     "traffic": traffic},
+                     "unit": "TOPS", "frac": round(tops_pw / INT8_PEAK_TOPS, 4),
+                     "traffic": traffic,
+                     "note": "int8 tera-operations per second issued by the pointwise kernel "
+                             "(dense int8 MFMA peak 5.0 POP/s)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

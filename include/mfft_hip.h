@@ -216,6 +216,14 @@ int  mfh_stage_times(const mfh_ctx *ctx, float ms[5]);
  * transforms, and those of the inverse + fold + carry (or decode) stages. */
 int  mfh_work(const mfh_ctx *ctx, double *int8_ops, double *fwd_bytes,
               double *inv_bytes);
+/* The pointwise step of the most recent product: ring products issued per
+ * evaluation point (K^2, or 3 (K/2)^2 with the Gauss split of the ring
+ * halves, the default where a Gauss kernel exists for K; MFH_POINTWISE=flat
+ * at mfh_create forces K^2) and int8 digit products per ring product (6 or
+ * 9).  No reference counterpart (the reference's plan counts its own n x n
+ * products, mfft_plan.nprod). */
+int  mfh_pointwise_info(const mfh_ctx *ctx, int *ring_products_per_point,
+                        int *digit_products);
 
 #ifdef __cplusplus
 }

@@ -668,6 +668,14 @@ int mfh_stage_times(const mfh_ctx *c, float ms[5])
     return MFH_OK;
 }
 
+int mfh_pointwise_info(const mfh_ctx *c, int *ring, int *digit)
+{
+    if (!c) return MFH_E_ARG;
+    if (ring) *ring = c->pwr == MFH_PW_GAUSS ? 3 * (c->K / 2) * (c->K / 2) : c->K * c->K;
+    if (digit) *digit = c->mode == MFH_MODE_K7 ? 6 : 9;
+    return MFH_OK;
+}
+
 int mfh_work(const mfh_ctx *c, double *ops, double *fwd, double *inv)
 {
     if (!c) return MFH_E_ARG;

@@ -102,6 +102,7 @@ def load(path=None):
         "mfh_copy_dev": ([vp, vp, vp, sz], i),
         "mfh_set_timing": ([vp, i], i), "mfh_stage_times": ([vp, C.POINTER(C.c_float)], i),
         "mfh_work": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double)], i),
+        "mfh_pointwise_info": ([vp, C.POINTER(C.c_int), C.POINTER(C.c_int)], i),
         "mfft_plan_init": ([pl, i, i], i), "mfft_plan_products": ([pl], C.c_longlong),
         "mfft_plan_init_rec": ([pl, i, i, i], i),
         "ssa_negconv": ([vp, vp, vp, i, i, i, i], None),
@@ -238,6 +239,13 @@ class Ctx:
         a, b, c = C.c_double(), C.c_double(), C.c_double()
         check(self.lib.mfh_work(self.h, C.byref(a), C.byref(b), C.byref(c)))
         return a.value, b.value, c.value
+
+    def pointwise_info(self):
+        """(ring products per point, int8 digit products per ring product) of
+        the most recent product"""
+        r, d = C.c_int(), C.c_int()
+        check(self.lib.mfh_pointwise_info(self.h, C.byref(r), C.byref(d)))
+        return r.value, d.value
 
     def sync(self):
         check(self.lib.mfh_sync(self.h), "mfh_sync")

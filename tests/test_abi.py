@@ -253,3 +253,9 @@ def test_bench_refuses_more_than_one_gpu():
 def test_bench_rejects_bad_sizes(args):
     r = _bench(*args)
     assert r.returncode == 2 and "power of two" in r.stderr
+
+
+@pytest.mark.parametrize("args", [("--sweep-width", "--n", "-5"), ("--sweep-n", "--width", "48")])
+def test_bench_sweeps_reject_bad_sizes(args):
+    r = _bench(*args)
+    assert r.returncode == 2 and "sweeps need" in r.stderr
