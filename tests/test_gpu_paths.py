@@ -219,6 +219,42 @@ def test_fused_decode_matches_separate_decode(gpu, orc, monkeypatch):
     assert np.array_equal(res[0][1], res[1][1])
 
 
+@pytest.mark.parametrize("force", [512, 1024, 2048, 4096, 8192])
+def test_fused_decode_every_plan(gpu, orc, monkeypatch, force):
+    """The fused fp64 decode of every specialised inverse plan ((NB, K) =
+    (16, 8), (16, 16), (32, 16), (32, 32), (64, 32) at grids of 512 .. 8192
+    bits), and the fp32 one where the grid takes fp32 entries, bit-equal to
+    the generic kernels' separate decode and to the oracle (n = 45: a
+    ragged last workgroup)."""
+    n = 45
+    print(f"[fused decode] force={force}", flush=True)
+    rng = np.random.default_rng(force)
+    A = np.ldexp(rng.uniform(1, 2, n * n) * rng.choice([-1, 1], n * n),
+                 rng.integers(-60, 61, n * n))
+    B = np.ldexp(rng.uniform(1, 2, n * n) * rng.choice([-1, 1], n * n),
+                 rng.integers(-60, 61, n * n))
+    oc = orc.fpx_d(A, B, n, force)
+    oa, ob = orc.fpx_planes(oc)
+    L, SA, SB = oc.L, oc.SA, oc.SB
+    want = orc.fpx_decode_f64_from(oc, orc.conv_mfft(oa, ob, n, L, orc.plan(L)))
+    orc.fpx_free(oc)
+    X = orc.fp32_rand(n * n, force, -30, 30)
+    Y = orc.fp32_rand(n * n, force + 1, -30, 30)
+    oc = orc.fpx(X, Y, n, force)
+    xa, xb = orc.fpx_planes(oc)
+    want32 = orc.fpx_decode_from(oc, orc.conv_mfft(xa, xb, n, L, orc.plan(L)))
+    orc.fpx_free(oc)
+    for generic in (False, True):
+        if generic:
+            monkeypatch.setenv("MFH_GENERIC_KERNELS", "1")
+        with gpu.Ctx(n, L) as ctx:
+            got = ctx.fpx_mm_f64(A, B, SA, SB)
+            got32 = ctx.fpx_mm(X, Y, SA, SB)
+        assert np.array_equal(got.view(np.uint64), want.view(np.uint64)), generic
+        assert np.array_equal(got32.view(np.uint32), want32.view(np.uint32)), generic
+    assert np.count_nonzero(want) > n * n // 2
+
+
 def test_device_generator_matches_host(gpu, orc, lib):
     n, L = 96, 32
     with gpu.Ctx(n, L) as ctx:
