@@ -149,6 +149,16 @@ int mfh_fpx_decode_ld(const int64_t *Cw, int n, int L, int SAB, long double *C);
 int mfh_fpx_decode_sig63(const int64_t *Cw, int n, int L, int SAB, int64_t *sig,
                          int32_t *ex);
 
+/* Faithful limb-window product of the fixed-point floats (the
+ * fp32/64->mfft-faithful rows, src/mlgemm.c:909-961, 1186-1250): Aw, Bw are
+ * the Lk window planes u0 .. u0+Lk-1 of two L-plane signed limb matrices
+ * (host); their exact product, one leaf GEMM for Lk = 1 or the MFFT
+ * convolution under `plan` (L = Lk) otherwise, is placed at plane 2 u0 of
+ * 2L-1 zero planes and decoded on the device at scale 2^-SAB into C (fp32,
+ * or fp64 when f64 != 0), n x n host. */
+int mfh_fpx_faithful(const int32_t *Aw, const int32_t *Bw, int n, int L, int u0, int Lk,
+                     const mfh_plan *plan, int SAB, int f64, void *C);
+
 /* ---- schoolbook: the leaf operator and the limb-plane method ------------
  * Integer-ALU kernels, exact modulo 2^64 for any int32 entries (the
  * reference's int64 leaves wrap the same way); an independent second

@@ -173,6 +173,24 @@ int  fpx_mm_f32(fpx_ctx *c, const mfft_plan *p, float *C);
  * conv_mfft + fpx_decode_f64 bit for bit; no reference counterpart) */
 int  fpx_mm_f64(fpx_ctx *c, const mfft_plan *p, double *C);
 
+/* Faithful limb window (src/mlgemm.c:593-630, static there): hi = the
+ * highest limb plane that is non-zero in A32 or B32 of an encoded context
+ * (L-1 when all are zero); the window is the top limb (Lk = 1) for
+ * max_keep <= 1, else the largest power of two Lk <= min(max_keep, hi+1, L)
+ * (at least 2 when hi >= 1); *u0 = hi - Lk + 1.  Returns Lk. */
+int  fpx_faithful_window(const fpx_ctx *c, int max_keep, int *u0, int *hi);
+/* The fp32/64->mfft-faithful products (src/mlgemm.c:1186-1250 fp32,
+ * :909-961 fp64) on the device, after fpx_encode / fpx_encode_d: the exact
+ * product of the window's planes (one leaf GEMM for Lk = 1, else conv_mfft
+ * under mfft_plan_init_rec for Lk >= 4 or mfft_plan_init, as there), placed
+ * at plane 2 u0 of 2L-1 zero planes and rounded once by the reference's
+ * decode into C (n x n).  Inexact by design: the planes below the window
+ * are dropped.  The window is reported in *Lk and *u0 (either may be NULL).
+ * c->Cw is not written.  Returns 0 or a negative MFH_E_* code (no reference
+ * counterpart as a function: the reference inlines these steps). */
+int  fpx_faithful_f32(fpx_ctx *c, int max_keep, float *C, int *Lk, int *u0);
+int  fpx_faithful_f64(fpx_ctx *c, int max_keep, double *C, int *Lk, int *u0);
+
 /* Status of the most recent call on this thread: 0, or a negative code
  * from mfft_hip.h (MFH_E_*). */
 int         mfft_last_error(void);

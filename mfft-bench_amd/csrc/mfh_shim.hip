@@ -919,6 +919,48 @@ int mfh_negconv(const int32_t *A, const int32_t *B, int K, int n, int64_t *C)
     return MFH_OK;
 }
 
+int mfh_fpx_faithful(const int32_t *Aw, const int32_t *Bw, int n, int L, int u0, int Lk,
+                     const mfh_plan *plan, int SAB, int f64, void *C)
+{
+    if (!Aw || !Bw || !C || n < 1 || L < 1 || Lk < 1 || u0 < 0 || u0 + Lk > L)
+        return MFH_E_ARG;
+    if (Lk > 1 && (!plan || plan->L != Lk)) return MFH_E_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    const size_t nn = (size_t)n * n, eb = f64 ? 8 : 4;
+    const size_t cw_b = (size_t)(2 * L - 1) * nn * 8;
+    TmpBufs t;
+    if (hipMalloc(&t.p[0], 2 * (size_t)Lk * nn * 4) != hipSuccess ||
+        hipMalloc(&t.p[1], cw_b) != hipSuccess || hipMalloc(&t.p[2], nn * eb) != hipSuccess)
+        return MFH_E_NOMEM;
+    int32_t *dA = (int32_t *)t.p[0], *dB = dA + (size_t)Lk * nn;
+    int64_t *dCw = (int64_t *)t.p[1], *dWin = dCw + (size_t)(2 * u0) * nn;
+    MFH_HIP(hipMemcpy(dA, Aw, (size_t)Lk * nn * 4, hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(dB, Bw, (size_t)Lk * nn * 4, hipMemcpyHostToDevice));
+    MFH_HIP(hipMemset(dCw, 0, cw_b));
+    if (Lk == 1) {
+        // the top planes' product, one leaf GEMM (src/mlgemm.c:1195-1197)
+        if ((rc = mfh_launch_mm_accum(dWin, dA, dB, n, 1, 0))) return rc;
+        MFH_HIP(hipDeviceSynchronize());
+    } else {
+        // the window's 2Lk-1 coefficient planes written in place at 2 u0
+        mfh_ctx *c = nullptr;
+        if ((rc = mfh_create(&c, n, Lk, plan))) return rc;
+        rc = mfh_conv_dev(c, dA, dB, dWin);
+        if (!rc) rc = mfh_sync(c);
+        mfh_destroy(c);
+        if (rc) return rc;
+    }
+    mfh_ctx bare;
+    bare_ctx(bare, n, L);
+    if ((rc = mfh_launch_decode(&bare, dCw, SAB, f64 ? MFH_DEC_F64 : MFH_DEC_F32, t.p[2],
+                                nullptr)))
+        return rc;
+    MFH_HIP(hipDeviceSynchronize());
+    MFH_HIP(hipMemcpy(C, t.p[2], nn * eb, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+
 int mfh_fpx_encode(const float *X, int n, int L, int S, int32_t *X32)
 {
     return encode_host(X, 0, n, L, S, X32);

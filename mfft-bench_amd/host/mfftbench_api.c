@@ -609,6 +609,69 @@ int fpx_mm_f64(fpx_ctx *c, const mfft_plan *p, double *C)
     return fpx_mm_common(c, p, C, 1, "fpx_mm_f64");
 }
 
+/* src/mlgemm.c:593-630: the window over the highest live limb planes */
+int fpx_faithful_window(const fpx_ctx *c, int max_keep, int *u0_out, int *hi_out)
+{
+    const size_t nn = (size_t)c->n * c->n;
+    int hi = -1;
+    for (int w = 0; w < c->L; w++) {
+        int any = 0;
+        for (size_t i = 0; i < nn && !any; i++)
+            if (c->A32[(size_t)w * nn + i] || c->B32[(size_t)w * nn + i]) any = 1;
+        if (any) hi = w;
+    }
+    if (hi < 0) hi = c->L - 1;
+    const int span = hi + 1;
+    int Lk = 1;
+    if (max_keep > 1) {
+        const int keep = max_keep < c->L ? max_keep : c->L;
+        while (Lk * 2 <= keep && Lk * 2 <= span && Lk * 2 <= c->L) Lk *= 2;
+        if (Lk < 2 && keep >= 2 && span >= 2) Lk = 2;
+    }
+    if (Lk > span) Lk = span;
+    if (Lk < 1) Lk = 1;
+    int u0 = hi - Lk + 1;
+    if (u0 < 0) u0 = 0;
+    if (u0_out) *u0_out = u0;
+    if (hi_out) *hi_out = hi;
+    return Lk;
+}
+
+static int faithful_common(fpx_ctx *c, int max_keep, void *C, int f64, int *Lk_out,
+                           int *u0_out, const char *name)
+{
+    t_last_error = 0;
+    if (!c || !c->A32 || !c->B32 || !C || (c->sig == 53) != (f64 != 0))
+        return fail(name, MFH_E_ARG);
+    int u0, hi;
+    const int Lk = fpx_faithful_window(c, max_keep, &u0, &hi);
+    mfft_plan p;
+    mfh_plan hp;
+    if (Lk >= 2) {
+        // src/mlgemm.c:1211-1213: the recursive plan from 4 limbs on
+        const int ok = Lk >= 4 ? mfft_plan_init_rec(&p, Lk, c->n, 0) : mfft_plan_init(&p, Lk, 0);
+        if (ok != 0) return fail(name, MFH_E_UNSUPPORTED);
+        hp = (mfh_plan){p.L, p.S, p.NB, p.K, p.g, 0, (long long)p.NB * p.K * p.K};
+    }
+    const size_t nn = (size_t)c->n * c->n;
+    int rc = mfh_fpx_faithful(c->A32 + (size_t)u0 * nn, c->B32 + (size_t)u0 * nn, c->n, c->L,
+                              u0, Lk, Lk >= 2 ? &hp : NULL, c->SA + c->SB, f64, C);
+    if (rc) return fail(name, rc);
+    if (Lk_out) *Lk_out = Lk;
+    if (u0_out) *u0_out = u0;
+    return 0;
+}
+
+int fpx_faithful_f32(fpx_ctx *c, int max_keep, float *C, int *Lk, int *u0)
+{
+    return faithful_common(c, max_keep, C, 0, Lk, u0, "fpx_faithful_f32");
+}
+
+int fpx_faithful_f64(fpx_ctx *c, int max_keep, double *C, int *Lk, int *u0)
+{
+    return faithful_common(c, max_keep, C, 1, Lk, u0, "fpx_faithful_f64");
+}
+
 /* src/fpfixed.c:324-328, plus the device copies kept for the context */
 void fpx_free(fpx_ctx *c)
 {

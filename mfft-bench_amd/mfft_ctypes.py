@@ -128,6 +128,10 @@ def load(path=None):
         "fpx_decode_f64": ([C.POINTER(FpxCtx), vp], None),
         "fpx_decode_ld": ([C.POINTER(FpxCtx), vp], None),
         "fpx_mm_f64": ([C.POINTER(FpxCtx), pl, vp], i),
+        "fpx_faithful_window": ([C.POINTER(FpxCtx), i, vp, vp], i),
+        "fpx_faithful_f32": ([C.POINTER(FpxCtx), i, vp, vp, vp], i),
+        "fpx_faithful_f64": ([C.POINTER(FpxCtx), i, vp, vp, vp], i),
+        "mfh_fpx_faithful": ([vp, vp, i, i, i, i, pl, i, i, vp], i),
         "mfft_profile_reset": ([], None), "mfft_profile_print": ([C.c_char_p], None),
         "mfft_last_error": ([], i), "mfft_strerror": ([i], C.c_char_p),
         "kernel_name": ([i], C.c_char_p), "kernel_from_name": ([C.c_char_p], i),

@@ -107,6 +107,14 @@ void orc_fpx_decode_f64_from(const orc_fpx *c, const int64_t *Cw, double *C);
 void orc_fpx_decode_sig63_from(const orc_fpx *c, const int64_t *Cw, int64_t *sig,
                                int32_t *ex);
 void orc_fpx_free(orc_fpx *c);
+/* The faithful limb window (src/mlgemm.c:593-630): returns Lk, sets *u0 and
+ * *hi from the planes of an encoded context. */
+int  orc_faithful_window(const orc_fpx *c, int max_keep, int *u0, int *hi);
+/* The faithful product's coefficient planes (src/mlgemm.c:909-961 fp64 with
+ * max_keep 2, :1186-1250 fp32): Cw (2L-1 planes) = 0 except the exact
+ * convolution of the window planes at plane 2 u0 (the schoolbook, which
+ * equals conv_mfft); returns Lk. */
+int  orc_faithful_cw(const orc_fpx *c, int max_keep, int64_t *Cw, int *u0);
 
 /* ---- checking helpers (not in the reference) ---------------------------- */
 /* fp32 inputs +-m*2^e, m~U[1,2) with 23 random fraction bits, e~U{emin..emax},

@@ -103,6 +103,8 @@ class Oracle:
         L.orc_fpx_encode_d.argtypes = [C.POINTER(OrcFpx), vp, vp]
         L.orc_fpx_decode_f64_from.argtypes = [C.POINTER(OrcFpx), vp, vp]
         L.orc_fpx_decode_sig63_from.argtypes = [C.POINTER(OrcFpx), vp, vp, vp]
+        L.orc_faithful_window.argtypes = [C.POINTER(OrcFpx), i, vp, vp]
+        L.orc_faithful_cw.argtypes = [C.POINTER(OrcFpx), i, vp, vp]
         L.orc_fp32_rand.argtypes = [vp, C.c_size_t, u64, i, i]
         L.orc_entry_exact.argtypes = [vp, vp, i, i, i, i, i, vp, i]
         L.orc_freivalds.argtypes = [vp, vp, i, i, i, vp, i, i, u64]
@@ -215,6 +217,19 @@ class Oracle:
 
     def fpx_free(self, ctx):
         self.lib.orc_fpx_free(C.byref(ctx))
+
+    def faithful_window(self, ctx, max_keep):
+        """(Lk, u0, hi) of the faithful limb window (src/mlgemm.c:593-630)"""
+        u0, hi = C.c_int(), C.c_int()
+        Lk = self.lib.orc_faithful_window(C.byref(ctx), max_keep, C.byref(u0), C.byref(hi))
+        return Lk, u0.value, hi.value
+
+    def faithful_cw(self, ctx, max_keep):
+        """the faithful product's 2L-1 coefficient planes, Lk, u0"""
+        cw = np.empty((2 * ctx.L - 1) * ctx.n * ctx.n, dtype=np.int64)
+        u0 = C.c_int()
+        Lk = self.lib.orc_faithful_cw(C.byref(ctx), max_keep, _p(cw), C.byref(u0))
+        return cw, Lk, u0.value
 
     # ---- checks -------------------------------------------------------------
     def entry_exact(self, A, B, n, L, i, j, RL, signed_top=False):

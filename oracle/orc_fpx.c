@@ -284,3 +284,39 @@ void orc_fpx_free(orc_fpx *c)
     free(c->A32); free(c->B32); free(c->Cw);
     c->A32 = NULL; c->B32 = NULL; c->Cw = NULL;
 }
+
+/* src/mlgemm.c:593-630 */
+int orc_faithful_window(const orc_fpx *c, int max_keep, int *u0, int *hi)
+{
+    const size_t nn = (size_t)c->n * c->n;
+    int top = -1;
+    for (int w = c->L - 1; w >= 0 && top < 0; w--)
+        for (size_t i = 0; i < nn; i++)
+            if (c->A32[(size_t)w * nn + i] != 0 || c->B32[(size_t)w * nn + i] != 0) {
+                top = w;
+                break;
+            }
+    if (top < 0) top = c->L - 1;
+    /* the largest power of two within max_keep, the live span and L; two
+       limbs at least when both are allowed; one for max_keep <= 1 */
+    int Lk = 1;
+    if (max_keep >= 2) {
+        while (2 * Lk <= max_keep && 2 * Lk <= top + 1 && 2 * Lk <= c->L) Lk *= 2;
+        if (Lk == 1 && top >= 1 && c->L >= 2) Lk = 2;
+    }
+    *u0 = top - Lk + 1 < 0 ? 0 : top - Lk + 1;
+    *hi = top;
+    return Lk;
+}
+
+/* src/mlgemm.c:909-961, 1186-1250 */
+int orc_faithful_cw(const orc_fpx *c, int max_keep, int64_t *Cw, int *u0)
+{
+    int hi;
+    const int Lk = orc_faithful_window(c, max_keep, u0, &hi);
+    const size_t nn = (size_t)c->n * c->n;
+    memset(Cw, 0, (size_t)(2 * c->L - 1) * nn * sizeof(int64_t));
+    orc_conv_limbplane(Cw + (size_t)(2 * *u0) * nn, c->A32 + (size_t)*u0 * nn,
+                       c->B32 + (size_t)*u0 * nn, c->n, Lk, 2);
+    return Lk;
+}
