@@ -1020,7 +1020,9 @@ bool mfh_gauss_supported(int K) { return K == 16; }
 
 int mfh_launch_pointwise(mfh_ctx *c, int rows)
 {
-    if (c->pw == MFH_PW_GAUSS) {
+    // the product's algorithm, set with its digit mode: the forward
+    // transform wrote Gauss slots only when pwr says so
+    if (c->pwr == MFH_PW_GAUSS) {
         switch (c->K) {
         // 64 x 32 tiles, 8 waves at 2 per SIMD, pairs read 4 ahead, barrier
         // after diagonal group 4, the next sub-round's first pairs read
