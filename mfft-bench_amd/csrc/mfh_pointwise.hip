@@ -337,11 +337,21 @@ __device__ __forceinline__ void round_barrier()
 // per CU).  When the tile grid allows, each such group of 512 covers a
 // 16 x 32 block of tiles of one point and the 64 workgroups of one XCD an
 // 8 x 8 sub-block of it, so that the operand tiles one XCD streams are
-// shared by 8 of its workgroups; otherwise tiles are taken in row order.
+// shared by 8 of its workgroups.  Small points (at most 256 tiles, the
+// point count a multiple of 8) go whole to one XCD: XCD x takes points x,
+// x + 8, .., each in row order, so that its resident workgroups share the
+// operand tiles of one point.  Otherwise tiles are taken in row order.
 __device__ __forceinline__ void tile_of(int tiles_j, int &ti, int &tj, int &jp)
 {
     const int per_point = gridDim.x, tiles_i = per_point / tiles_j;
-    if (tiles_i % 16 == 0 && tiles_j % 32 == 0) {
+    if (per_point <= 256 && gridDim.y % 8 == 0) {
+        const int w = blockIdx.y * per_point + blockIdx.x;
+        const int x = w & 7, q = w >> 3;
+        jp = (q / per_point) * 8 + x;
+        const int t = q % per_point;
+        ti = t / tiles_j;
+        tj = t % tiles_j;
+    } else if (tiles_i % 16 == 0 && tiles_j % 32 == 0) {
         const int w = blockIdx.y * per_point + blockIdx.x;
         const int x = w & 7, q = w >> 3;
         const int g = q >> 6, ql = q & 63;            // group of 512, slot within XCD
@@ -691,11 +701,22 @@ int launch_cfg(mfh_ctx *c, int rows)
 // complete by then), the wave reads the first D pairs of the next
 // sub-round, so that its first MFMAs do not wait for LDS.
 // ============================================================================
-template <int K_, int WBI_, int WBJ_, int WPE_, int D_, int BAR_, int PRE_, bool SPLIT_ = false>
+//
+// NSLOT = 2 (rings whose three slots do not fit in LDS): sub-round u lives
+// in slot u mod 2, so the slot of sub-round g alternates with the parity of
+// the round.  After the diagonal group BAR of sub-round u (its last read of
+// the slot done) a barrier follows and the copies of sub-round u+2 go into
+// the slot; after the group PRE > BAR the wave waits for its copies of
+// sub-round u+1 (only the ones just issued may stay in flight), a second
+// barrier follows, and the first pairs of sub-round u+1 are read.  Copies
+// thus have one sub-round plus PRE - BAR diagonal groups to land.
+template <int K_, int WBI_, int WBJ_, int WPE_, int D_, int BAR_, int PRE_, bool SPLIT_ = false,
+          int NSLOT_ = 3>
 struct GsCfg {
     static constexpr int K = K_, H = K_ / 2, WBI = WBI_, WBJ = WBJ_, WPE = WPE_;
     static constexpr int D = D_, BAR = BAR_, PRE = PRE_;
     static constexpr bool SPLIT = SPLIT_;
+    static constexpr int NSLOT = NSLOT_;
     static constexpr int WAVES = WBI * WBJ, THREADS = WAVES * 64;
     static constexpr int BI = 16 * WBI, BJ = 16 * WBJ;
     static constexpr int A_CHUNKS = H * WBI * 64, B_CHUNKS = H * WBJ * 64;   // one sub-round
@@ -711,8 +732,9 @@ struct GsCfg {
     static_assert(BAR % 2 == 0 && BAR > LAST_READ && BAR < ND, "barrier after the last read");
     static_assert(PRE % 2 == 0 && PRE >= BAR && PRE < ND, "prefetch after the barrier");
     static_assert(!SPLIT || PRE > BAR, "split barrier: arrive before waiting");
-    static_assert(NPW < 16, "vmcnt immediate");
-    static_assert(3 * (A_CHUNKS + B_CHUNKS) * 16 <= 160 * 1024, "three slots fit in LDS");
+    static_assert(NSLOT == 2 || NPW < 16, "vmcnt immediate");
+    static_assert(NSLOT == 2 || NSLOT == 3, "two or three LDS slots");
+    static_assert(NSLOT * (A_CHUNKS + B_CHUNKS) * 16 <= 160 * 1024, "the slots fit in LDS");
 };
 
 // s_waitcnt vmcnt(V) lgkmcnt(0) (expcnt left alone)
@@ -721,6 +743,14 @@ __device__ __forceinline__ void vm_lgkm_wait()
 {
     static_assert(V >= 0 && V < 16, "4-bit vmcnt field");
     __builtin_amdgcn_s_waitcnt((V & 15) | (7 << 4) | (0 << 8));
+}
+// s_waitcnt vmcnt(V) lgkmcnt(0) for V up to 63 (gfx9: vmcnt bits 3:0 and
+// 15:14)
+template <int V>
+__device__ __forceinline__ void vm_lgkm_wait6()
+{
+    static_assert(V >= 0 && V < 64, "6-bit vmcnt");
+    __builtin_amdgcn_s_waitcnt((V & 15) | (7 << 4) | (0 << 8) | ((V >> 4) << 14));
 }
 // the same, then a workgroup barrier
 template <int V>
@@ -1012,11 +1042,178 @@ int launch_gauss(mfh_ctx *c, int rows)
     return MFH_OK;
 }
 
+// Two-slot Gauss kernel (Cfg::NSLOT == 2): the three sub-rounds of a round
+// of parity P live in slots P, 1-P, P.  Rounds run in one sequence over all
+// classes; (m, rd) is the current round and (nm, nrd) the next one (the
+// last round itself at the end, so that every sub-round issues the same
+// copies: the slot they land in is never read again).
+template <class Cfg, int MODE>
+__global__ void __attribute__((amdgpu_flat_work_group_size(Cfg::THREADS, Cfg::THREADS),
+                               amdgpu_waves_per_eu(Cfg::WPE, Cfg::WPE)))
+k_pointwise_gauss2(const int8_t *__restrict__ Ah, const int8_t *__restrict__ Bh,
+                   int32_t *__restrict__ C5, int np_, int rows, int tiles_j)
+{
+    static_assert(Cfg::NSLOT == 2, "two-slot schedule");
+    static_assert(MODE == MFH_MODE_K7, "one digit pair per class");
+    static_assert(Cfg::PRE > Cfg::BAR && !Cfg::SPLIT, "two barriers per sub-round");
+    constexpr int K = Cfg::K, H = Cfg::H, WBI = Cfg::WBI, WBJ = Cfg::WBJ, W = Cfg::WAVES;
+    constexpr int NA = Cfg::NA, NBF = Cfg::NBF;
+    constexpr int NCLASS = MODE == MFH_MODE_K7 ? 6 : 2 * MFH_DIGITS - 1;
+    constexpr int PL = MODE == MFH_MODE_K7 ? 6 : MFH_DIGITS;     // planes per slot
+    constexpr int NSL = 3 * H;                                    // slots per point
+    __shared__ v4i sA0[Cfg::A_CHUNKS], sA1[Cfg::A_CHUNKS];
+    __shared__ v4i sB0[Cfg::B_CHUNKS], sB1[Cfg::B_CHUNKS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wbi = wave / WBJ, wbj = wave % WBJ;
+    int ti, tj, jp;
+    tile_of(tiles_j, ti, tj, jp);
+    const int i0 = ti * Cfg::BI, j0 = tj * Cfg::BJ;
+    const size_t plane = (size_t)np_ * np_;
+    const size_t planeA = (size_t)rows * np_;
+    const int8_t *Aj = Ah + (size_t)jp * NSL * PL * planeA;
+    const int8_t *Bj = Bh + (size_t)jp * NSL * PL * plane;
+    const int8_t *a_blk = Aj + (size_t)(wave / WBI) * PL * planeA +
+                          mfh_tile_off(i0 + (wave % WBI) * 16, 0, np_) + (lane & 15) * 64 +
+                          (lane >> 4) * 16;
+    const int8_t *b_blk = Bj + (size_t)(wave / WBJ) * PL * plane +
+                          mfh_tile_off(j0 + (wave % WBJ) * 16, 0, np_) + (lane & 15) * 64 +
+                          (lane >> 4) * 16;
+    const size_t da = (size_t)(W / WBI) * PL * planeA;
+    const size_t db = (size_t)(W / WBJ) * PL * plane;
+    const int kblocks = np_ / MFH_KBLK;
+    const int col = j0 + wbj * 16 + (lane & 15);
+    const int row0 = i0 + wbi * 16 + 4 * (lane >> 4);
+
+    // copies of sub-product G of round rd of class m into slot SL
+    auto copy = [&](auto gtag, auto stag, int m, int rd) {
+        constexpr int G = decltype(gtag)::value, SL = decltype(stag)::value;
+        v4i *dA = SL == 0 ? sA0 : sA1;
+        v4i *dB = SL == 0 ? sB0 : sB1;
+        int rlo, npr;
+        class_pairs<MODE>(m, rlo, npr);
+        const int r = rlo + rd / kblocks, kb = rd % kblocks;
+        const int s = MODE == MFH_MODE_K7 ? r : m - r;
+        const int8_t *a0 = a_blk + ((size_t)G * H * PL + r) * planeA + kb * 1024;
+        const int8_t *b0 = b_blk + ((size_t)G * H * PL + s) * plane + kb * 1024;
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(a0 + i * da),
+                                             (void *)(dA + (wave + i * W) * 64), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NBF; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(b0 + i * db),
+                                             (void *)(dB + (wave + i * W) * 64), 16, 0, 0);
+    };
+    using G0 = std::integral_constant<int, 0>;
+    using G1 = std::integral_constant<int, 1>;
+    using G2 = std::integral_constant<int, 2>;
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+
+    // prologue: sub-rounds 0 and 1 of round 0 of class 0 (slots 0 and 1)
+    copy(G0{}, S0{}, 0, 0);
+    copy(G1{}, S1{}, 0, 0);
+    vm_lgkm_barrier<0>();
+
+    v4i acc[K], ng[H - 1];
+    constexpr int D = Cfg::D;
+    v4i pa[D], pb[D];          // the first pairs of the next sub-round
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+        pa[c] = sA0[(c * WBI + wbi) * 64 + lane];
+        pb[c] = sB0[(c * WBJ + wbj) * 64 + lane];
+    }
+    // sub-round G in slot SL; its copies are sub-product TG of round
+    // (tm, trd), into slot SL once every wave is done reading it
+    auto sub = [&](auto gtag, auto stag, auto tgtag, int tm, int trd) {
+        constexpr int G = decltype(gtag)::value, SL = decltype(stag)::value;
+        const v4i *la = (SL == 0 ? sA0 : sA1) + wbi * 64 + lane;
+        const v4i *lb = (SL == 0 ? sB0 : sB1) + wbj * 64 + lane;
+        const v4i *nla = (SL == 0 ? sA1 : sA0) + wbi * 64 + lane;
+        const v4i *nlb = (SL == 0 ? sB1 : sB0) + wbj * 64 + lane;
+        gs_sub<Cfg, G>(acc, ng, pa, pb, la, lb, nla, nlb, [&](int s0) {
+            if (s0 == Cfg::BAR) {
+                // every wave has read its last pair of this slot: refill it
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                copy(tgtag, stag, tm, trd);
+            } else if (s0 == Cfg::PRE) {
+                // every wave's copies of the next sub-round have landed
+                // (those just issued may still be in flight)
+                vm_lgkm_wait6<Cfg::NPW>();
+                __builtin_amdgcn_s_barrier();
+            }
+        });
+    };
+    // one round of parity P
+    auto round = [&](auto ptag, int m, int rd, int nm, int nrd) {
+        constexpr int P = decltype(ptag)::value;
+        using SP = std::integral_constant<int, P>;
+        using SQ = std::integral_constant<int, 1 - P>;
+        sub(G0{}, SP{}, G2{}, m, rd);
+        sub(G1{}, SQ{}, G0{}, nm, nrd);
+        sub(G2{}, SP{}, G1{}, nm, nrd);
+    };
+    auto zero = [&]() {
+#pragma unroll
+        for (int t = 0; t < K; ++t) acc[t] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < H - 1; ++t) ng[t] = v4i{0, 0, 0, 0};
+    };
+    // after round R: a class that ends there is stored and C restarts
+    auto finish = [&](int R) {
+        if ((R + 1) % kblocks) return;
+        const int m = R / kblocks;
+#pragma unroll
+        for (int t = 0; t < H - 1; ++t) acc[t] -= ng[t];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+#pragma unroll
+            for (int tt = 0; tt < K; tt += 4) {
+                const v4i qv = {acc[tt][v], acc[tt + 1][v], acc[tt + 2][v], acc[tt + 3][v]};
+                __builtin_nontemporal_store(
+                    qv, (v4i *)(C5 + mfh_c5_index(jp, row0 + v, col, tt, np_, NCLASS, K, rows) +
+                                (size_t)m * mfh_c5_class_stride(np_, K)));
+            }
+        }
+        zero();
+    };
+    // K7: one digit pair per class, so round R is k block R mod kblocks of
+    // class R / kblocks, and the 6 kblocks rounds pair up into parities
+    // 0, 1 with no branch between the two round bodies
+    const int total = NCLASS * kblocks;
+    zero();
+#pragma unroll 1
+    for (int R = 0; R < total; R += 2) {
+        round(S0{}, R / kblocks, R % kblocks, (R + 1) / kblocks, (R + 1) % kblocks);
+        finish(R);
+        const int n1 = R + 2 < total ? R + 2 : R + 1;
+        round(S1{}, (R + 1) / kblocks, (R + 1) % kblocks, n1 / kblocks, n1 % kblocks);
+        finish(R + 1);
+    }
+    // the last round's copies into LDS complete before the workgroup ends
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));
+}
+
+template <class Cfg>
+int launch_gauss2(mfh_ctx *c, int rows)
+{
+    if (c->np % MFH_KBLK || rows % Cfg::BI || c->np % Cfg::BJ || rows < 1 || rows > c->np)
+        return MFH_E_UNSUPPORTED;
+    const int tiles_i = rows / Cfg::BI, tiles_j = c->np / Cfg::BJ;
+    if (c->mode != MFH_MODE_K7) return MFH_E_UNSUPPORTED;
+    dim3 grid((unsigned)(tiles_i * tiles_j), (unsigned)c->NB);
+    hipLaunchKernelGGL((k_pointwise_gauss2<Cfg, MFH_MODE_K7>), grid, dim3(Cfg::THREADS), 0,
+                       c->stream, c->dAh, c->dBh, c->dC5, c->np, rows, tiles_j);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
 }  // namespace
 
 // K values with a Gauss kernel (the forward transform writes Gauss slots
 // only for these)
-bool mfh_gauss_supported(int K) { return K == 16; }
+bool mfh_gauss_supported(int K) { return K == 16 || K == 32; }
 
 int mfh_launch_pointwise(mfh_ctx *c, int rows)
 {
@@ -1028,6 +1225,12 @@ int mfh_launch_pointwise(mfh_ctx *c, int rows)
         // after diagonal group 4, the next sub-round's first pairs read
         // after group 8
         case 16: return launch_gauss<GsCfg<16, 4, 2, 2, 4, 4, 8, true>>(c, rows);
+        // 32 x 32 tiles, 4 waves at 1 per SIMD, two 64 KiB slots, pairs
+        // read 4 ahead, slot refilled after diagonal group 12, the next
+        // sub-round's copies waited for after group 24 (4.30 -> 4.18 ms
+        // at n = 256 with whole points per XCD, against 4.58 for the flat
+        // kernel)
+        case 32: return launch_gauss2<GsCfg<32, 2, 2, 1, 4, 12, 24, false, 2>>(c, rows);
         default: return MFH_E_UNSUPPORTED;
         }
     }

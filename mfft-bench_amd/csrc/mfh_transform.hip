@@ -1362,7 +1362,7 @@ bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_mode, int row0, int
     if (gs == 0)
         return try_fast1<S, NB, MODE, RECODE, Src, Limbs, E, Q, XB, 0>(c, s, dst, top_mode,
                                                                          row0, rows);
-    if constexpr (MODE == MFH_MODE_K7 && 2 * S == 16) {
+    if constexpr (MODE == MFH_MODE_K7 && (2 * S == 16 || 2 * S == 32)) {
         if (gs == 1)
             return try_fast1<S, NB, MODE, RECODE, Src, Limbs, E, Q, XB, 1>(c, s, dst, top_mode,
                                                                              row0, rows);
