@@ -90,6 +90,31 @@ int mfh_mm(mfh_ctx *ctx, int in_kind, const uint16_t *A, const uint16_t *B,
 int mfh_conv(mfh_ctx *ctx, const int32_t *A32, const int32_t *B32,
              int64_t *Cw);
 
+/* Intermediate results of mfh_conv's device path, for inspection and
+ * stage-level tests (no reference counterpart: the reference's stages are
+ * static functions of src/mfft.c).  The product of A32 and B32 runs up to
+ * `stage` for row band 0 and the raw device buffer is copied to out:
+ *   MFH_STAGE_A: A's int8 digit planes, [NB][slots][planes] planes of
+ *     rows x np entries in 16 x 64 tiles (tile (i/16, k/64) row-major, each
+ *     tile row-major); point j is the transform's point j (omega^j), in
+ *     natural order; slots are the K ring coefficients, or under the Gauss
+ *     pointwise the 3K/2 slots [z0+z1 | z0 | z1] (z0, z1 the coefficient
+ *     halves); planes are the digits of the digit mode;
+ *   MFH_STAGE_B: the same for B^T (entry (j', k) = B[k][j']) over np rows,
+ *     Gauss slots [z0 | z1-z0 | -(z0+z1)];
+ *   MFH_STAGE_CLASSES: the int32 class results of the pointwise step,
+ *     C[j][i][m][j'/16][t/4][j'%16][t%4], K np ints per (j, i, m).
+ * info[0..4] = digit mode (0: three balanced base-2^8 digits, 5 classes of
+ * 9 products; 1: three balanced base-2^7 digits and their pairwise sums, 6
+ * Karatsuba products), pointwise algorithm (0 flat, 1 Gauss), band rows,
+ * np, bytes of the stage; with out NULL only info is filled.  Returns 0,
+ * or MFH_E_ARG when out_bytes is short. */
+#define MFH_STAGE_A 0
+#define MFH_STAGE_B 1
+#define MFH_STAGE_CLASSES 2
+int mfh_conv_stages(mfh_ctx *ctx, const int32_t *A32, const int32_t *B32, int stage,
+                    void *out, size_t out_bytes, int64_t info[5]);
+
 /* ---- device-buffer entry points (stream-ordered, no sync) --------------- */
 /* dA and dB must be 16-byte aligned (the limbs are read 8 at a time; any
  * hipMalloc pointer is): MFH_E_ARG otherwise, before any kernel runs. */

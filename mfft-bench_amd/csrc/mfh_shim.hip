@@ -561,6 +561,50 @@ int mfh_conv(mfh_ctx *c, const int32_t *A32, const int32_t *B32, int64_t *Cw)
     return MFH_OK;
 }
 
+int mfh_conv_stages(mfh_ctx *c, const int32_t *A32, const int32_t *B32, int stage, void *out,
+                    size_t out_bytes, int64_t *info)
+{
+    if (!c || !A32 || !B32 || !info || stage < MFH_STAGE_A || stage > MFH_STAGE_CLASSES)
+        return MFH_E_ARG;
+    if (!conv_size_ok(c)) return MFH_E_BOUND;
+    const size_t nn = (size_t)c->n * c->n;
+    const size_t in_b = (size_t)c->L * nn * 4;
+    int rc = ensure_staging(c, in_b, 0), flag = 0;
+    if (rc) return rc;
+    const int rows = c->hb < c->np ? c->hb : c->np;        // row band 0
+    const size_t planes = (size_t)c->NB * mfh_slots(c->K, c->pwr) * mfh_planes(c->mode);
+    const size_t bytes = stage == MFH_STAGE_A   ? planes * rows * c->np
+                         : stage == MFH_STAGE_B ? planes * c->np * c->np
+                                                : (size_t)c->NB * rows * mfh_nclasses(c->mode) *
+                                                      mfh_c5_class_stride(c->np, c->K) * 4;
+    info[0] = c->mode;
+    info[1] = c->pwr;
+    info[2] = rows;
+    info[3] = c->np;
+    info[4] = (int64_t)bytes;
+    if (!out) return MFH_OK;
+    if (out_bytes < bytes) return MFH_E_ARG;
+    MFH_HIP(hipMemcpyAsync(c->dInA, A32, in_b, hipMemcpyHostToDevice, c->stream));
+    MFH_HIP(hipMemcpyAsync(c->dInB, B32, in_b, hipMemcpyHostToDevice, c->stream));
+    MFH_HIP(hipMemsetAsync(c->dFlag, 0, sizeof(int), c->stream));
+    if ((rc = mfh_launch_check_i32(c, (const int32_t *)c->dInA, c->L)) ||
+        (rc = mfh_launch_check_i32(c, (const int32_t *)c->dInB, c->L)) ||
+        (rc = read_flag(c, &flag)))
+        return rc;
+    if (flag) return MFH_E_RANGE;
+    select_mode(c, -1);
+    if ((rc = mfh_launch_transpose(c->dInB, c->dBt, c->L, c->n, 4, c->stream)) ||
+        (rc = mfh_launch_forward(c, MFH_IN_I32, c->dBt, c->dBh, 0, 0, c->np, 1)) ||
+        (rc = mfh_launch_forward(c, MFH_IN_I32, c->dInA, c->dAh, 0, 0, rows, 0)))
+        return rc;
+    if (stage == MFH_STAGE_CLASSES && (rc = mfh_launch_pointwise(c, rows))) return rc;
+    const void *src = stage == MFH_STAGE_A ? (const void *)c->dAh
+                      : stage == MFH_STAGE_B ? (const void *)c->dBh : (const void *)c->dC5;
+    MFH_HIP(hipMemcpyAsync(out, src, bytes, hipMemcpyDeviceToHost, c->stream));
+    MFH_HIP(hipStreamSynchronize(c->stream));
+    return MFH_OK;
+}
+
 namespace {
 int fpx_mm_host(mfh_ctx *c, int f64, const void *A, const void *B, int SA, int SB, void *C)
 {

@@ -103,6 +103,7 @@ def load(path=None):
         "mfh_set_timing": ([vp, i], i), "mfh_stage_times": ([vp, C.POINTER(C.c_float)], i),
         "mfh_work": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double)], i),
         "mfh_pointwise_info": ([vp, C.POINTER(C.c_int), C.POINTER(C.c_int)], i),
+        "mfh_conv_stages": ([vp, vp, vp, i, vp, sz, C.POINTER(C.c_int64)], i),
         "mfft_plan_init": ([pl, i, i], i), "mfft_plan_products": ([pl], C.c_longlong),
         "mfft_plan_init_rec": ([pl, i, i, i], i),
         "ssa_negconv": ([vp, vp, vp, i, i, i, i], None),
@@ -253,6 +254,17 @@ class Ctx:
 
     def sync(self):
         check(self.lib.mfh_sync(self.h), "mfh_sync")
+
+    def stages(self, A32, B32, stage):
+        """(info, raw bytes) of one stage of the conv product (mfh_conv_stages):
+        info = (digit mode, pointwise algorithm, band rows, np, bytes)"""
+        info = (C.c_int64 * 5)()
+        check(self.lib.mfh_conv_stages(self.h, _p(A32), _p(B32), stage, None, 0, info),
+              "mfh_conv_stages")
+        out = np.empty(int(info[4]), dtype=np.uint8)
+        check(self.lib.mfh_conv_stages(self.h, _p(A32), _p(B32), stage, _p(out), out.size,
+                                       info), "mfh_conv_stages")
+        return tuple(int(v) for v in info), out
 
 
 class DevBuf:

@@ -173,6 +173,13 @@ class Oracle:
         self.lib.orc_ring_dft(_p(X), _p(x), NB, K, g, direction)
         return X
 
+    def fft_forward32(self, X, NB, K, g, nn):
+        """in place: NB*K int32 planes of nn values, natural -> bit-reversed
+        point order (src/mfft.c:173-258)"""
+        assert X.dtype == np.int32 and X.flags.c_contiguous and X.size == NB * K * nn
+        self.lib.orc_fft_forward32(_p(X), NB, K, g, nn)
+        return X
+
     # ---- fp32 ----------------------------------------------------------------
     def fpx(self, A, B, n, force_bits):
         """encode A, B; returns (ctx, A32, B32) with numpy views of the planes"""
