@@ -658,9 +658,15 @@ __device__ __forceinline__ void forward_parts(int part, const Limbs &x, int8_t *
 // XB > 0: staged digit stores through XB LDS buffers (E = 256 only; the
 // band's element count must be a multiple of 256, so every thread of every
 // workgroup has an element and reaches every barrier).
+// At least two waves per SIMD: the W = 8192 kernels (81 KB of LDS, two
+// workgroups per CU fit) otherwise take 256+ registers and run one wave per
+// SIMD; capped at 256 they spill a few registers to scratch and write the
+// 48 Gauss slots 1.29 -> 1.02 ms faster per product at n = 256 (no change
+// for the 32 coefficient slots or the other plans, which fit already).
 template <int S, int NB, int Q, int MODE, bool RECODE, class Limbs, class Src, int E = 256,
           int XB = 0, int GS = 0>
-__global__ __launch_bounds__(256) void k_forward_fast(Src src, int8_t *__restrict__ out, int np_,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_forward_fast(
+    Src src, int8_t *__restrict__ out, int np_,
                                                       int top_mode, int row0, int rows)
 {
     constexpr int L = NB * S / 2;
