@@ -194,7 +194,8 @@ def method_table(args):
     methods on one exact-track workload: the schoolbook (limbplane, the
     speedup baseline as in src/main.c:293-297), the flat MFFT plan and the
     recursive plan (and, at K = 16, the flat plan with the K^2-product
-    pointwise kernel forced).  `products` is each method's n x n product
+    pointwise kernel forced); limbplane-mma is the schoolbook on the int8
+    matrix cores.  `products` is each method's n x n product
     count as the reference defines it (mfft_plan.nprod); `issued` is the
     ring products the device issued (NB times the per-point count of
     mfh_pointwise_info; each is 6 or 9 int8 digit GEMMs); `kernel_calls` is
@@ -238,6 +239,20 @@ def method_table_for(n, W, ekind, args, header=True):
                                                           dCw.ptr, dRef.ptr, RL)), 2)
     ref_out = dRef.download(np.uint16, RL * n * n)
     rows.append(["limbplane", "hip", L * L, L * L, 0, secs, ref_out])
+    # the same schoolbook on the matrix cores (limb pairs issued in blocks
+    # of 16 limbs, each 6 int8 digit GEMMs)
+    wbytes = M.C.c_size_t()
+    if lib.mfh_schoolbook_workspace(n, L, M.C.byref(wbytes)) == 0:
+        dW = M.DevBuf(wbytes.value)
+        secs = timed(lambda: M.check(lib.mfh_schoolbook_dev(None, kind, dA.ptr, dB.ptr, n, L,
+                                                            dW.ptr, wbytes.value, dO.ptr, RL)),
+                     max(1, min(args.steps, 3)))
+        dW.free()
+        nu16 = (L + 15) // 16 * 16
+        rows.append(["limbplane-mma", "hip", L * L, nu16 * nu16, 0, secs,
+                     dO.download(np.uint16, RL * n * n)])
+    else:
+        log(f"[table] limbplane-mma n={n} W={W}: outside its partial-sum bound")
     variants = [("mfft", M.plan(L), False), ("mfft-rec", M.plan_rec(L, n), False)]
     if M.plan(L) is not None and M.plan(L).K == 16:
         # the K^2-product kernel beside the default Gauss one at this ring

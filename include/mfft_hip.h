@@ -209,6 +209,26 @@ int mfh_limbplane_mm(const uint16_t *A, const uint16_t *B, int n, int L, uint16_
 int mfh_limbplane_mm_dev(mfh_ctx *ctx, int in_kind, const void *dA, const void *dB, int n,
                          int L, void *dCw, void *dOut, int RL);
 
+/* The same schoolbook on the int8 matrix cores (src/methods.c:94-123, the
+ * products formed otherwise): every uint16 limb (the top one as int16 with
+ * MFH_IN_U16_SIGNED) is split into the six int8 planes of its balanced
+ * base-2^7 digits and pair sums, the planes of each Karatsuba class are
+ * convolved over the limb axis with v_mfma_i32_16x16x64_i8 in blocks of 16
+ * limbs (6 L^2 int8 n^3 GEMMs), and the classes are recombined and carried.
+ * Out: RL > 0, RL uint16 limbs as mfh_limbplane_mm; RL = 0, the 2L-1 int64
+ * coefficient planes as mfh_limbplane_conv.  The int32 partial sums are
+ * exact modulo 2^32 and lie in a known range, which needs
+ * 16 ceil(L/16) n 32640 < 2^32, i.e. ceil(L/16) n <= 8224 (MFH_E_BOUND
+ * otherwise): n = 1024 at 2048 bits, 256 at 8192, 4096 at 512 bits
+ * pass.  mfh_schoolbook_workspace gives the
+ * bytes of device workspace mfh_schoolbook_dev needs; the host-buffer form
+ * allocates its own. */
+int mfh_schoolbook_workspace(int n, int L, size_t *bytes);
+int mfh_schoolbook_dev(mfh_ctx *ctx, int in_kind, const void *dA, const void *dB, int n, int L,
+                       void *dWork, size_t work_bytes, void *dOut, int RL);
+int mfh_schoolbook(int in_kind, const uint16_t *A, const uint16_t *B, int n, int L, void *out,
+                   int RL);
+
 /* mm_bigint_ijk / mm_bigint_ikj (src/methods.c:22-86): entry-major uint16
  * inputs (Aem[(i*n + k)*L + u]), plane-major RL-limb output; on the device
  * the inputs are re-laid plane-major and multiplied by the schoolbook */

@@ -212,6 +212,17 @@ int mfh_launch_mm_accum(int64_t *C, const int32_t *A, const int32_t *B, int n, i
                         hipStream_t st);
 int mfh_launch_conv_limbplane(int64_t *Cw, const void *A, const void *B, int in_kind, int n,
                               int L, hipStream_t st);
+// the schoolbook on the matrix cores: K7 digit planes of NLp >= L limbs
+// (16 x 64 tiles over np x np), the int32 partials P[6][2NU-1][np][np][32]
+// of the 16-limb block pairs (mfh_pointwise.hip), and their recombination
+// into 2L-1 int64 planes (Cw) or RL carried uint16 limbs (out); lo: the
+// lower end of every partial's range (width below 2^32)
+int mfh_launch_sb_digits(const void *src, int in_kind, int8_t *out, int n, int np_, int L,
+                         int NLp, hipStream_t st);
+int mfh_launch_schoolbook(const int8_t *Ad, const int8_t *Bd, int32_t *P, int np_, int NU,
+                          hipStream_t st);
+int mfh_launch_sb_combine(const int32_t *P, int64_t *Cw, uint16_t *out, int RL, int n, int np_,
+                          int L, int NU, long long lo, hipStream_t st);
 // entry-major uint16 limbs (e[idx*L + u]) -> plane-major
 int mfh_launch_entry_to_plane(const uint16_t *e, uint16_t *p, int n, int L, hipStream_t st);
 // C[t] = lin[t] - lin[t+K], t < K (negacyclic fold of 2K-1 planes)

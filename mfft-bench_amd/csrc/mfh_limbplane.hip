@@ -174,6 +174,114 @@ __global__ __launch_bounds__(256) void k_entry_to_plane(const uint16_t *__restri
     }
 }
 
+// ---- the schoolbook on the matrix cores (k_schoolbook, mfh_pointwise.hip) --
+// K7 digit planes of uint16 limbs (the top one read as int16 for two's
+// complement entries): out[u][p][tile order of (i, k)] for limbs
+// u < NLp (zero from L on) and i, k < np (zero outside n x n); plane u of
+// the source holds entry (i, k) at u*n*n + i*n + k (B is transposed first).
+// One thread per 4 consecutive k of a row: one dword of each plane.
+template <class T>
+__global__ __launch_bounds__(256) void k_sb_digits(const T *__restrict__ src,
+                                                   int8_t *__restrict__ out, int n, int np_,
+                                                   int L, int NLp, int sgn_top)
+{
+    const size_t per_plane = (size_t)np_ * np_ / 4;
+    const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= (size_t)NLp * per_plane) return;
+    const int u = (int)(q / per_plane);
+    const size_t e4 = (q % per_plane) * 4;
+    int i, k;
+    mfh_tile_ik(e4, np_, i, k);
+    const size_t nn = (size_t)n * n;
+    uint32_t w[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        int v = 0;
+        if (u < L && i < n && k + d < n)
+            v = load_in(src, (size_t)u * nn + (size_t)i * n + k + d, sgn_top && u == L - 1);
+        const int d0 = ((v + 64) & 127) - 64;
+        const int v1 = (v + 64) >> 7;
+        const int d1 = ((v1 + 64) & 127) - 64;
+        const int d2 = (v1 + 64) >> 7;
+        const int dg[6] = {d0, d1, d2, d0 + d1, d0 + d2, d1 + d2};
+#pragma unroll
+        for (int p = 0; p < 6; ++p) w[p] |= (uint32_t)(uint8_t)(int8_t)dg[p] << (8 * d);
+    }
+    const size_t plane = (size_t)np_ * np_;
+#pragma unroll
+    for (int p = 0; p < 6; ++p) *(uint32_t *)(out + ((size_t)u * 6 + p) * plane + e4) = w[p];
+}
+
+// Cw[w] = sum_m coef_m Q_m[w], Q_m[w] = P[m][w/16][w%16] + P[m][w/16-1][w%16+16]
+// (the Karatsuba recombination of the 6 classes is linear); each int32
+// partial is the residue mod 2^32 of a value in [lo, lo + 2^32).  One
+// thread per element walks w upwards: with Cw set it writes the 2L-1
+// coefficient planes, else it carries them into RL uint16 limbs (the
+// arithmetic-shift carry of normalize_planes, src/bigmat.c:48-60).
+__global__ __launch_bounds__(256) void k_sb_combine(const int32_t *__restrict__ P,
+                                                    long long *__restrict__ Cw,
+                                                    uint16_t *__restrict__ out, int RL, int n,
+                                                    int np_, int L, int NU, long long lo)
+{
+    const size_t nn = (size_t)n * n;
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= nn) return;
+    const int i = (int)(e / n), j = (int)(e % n);
+    const int NW = 2 * NU - 1, P2 = 2 * L - 1;
+    const long long coef[6] = {1 - 128 - 16384, -128 + 16384 - 2097152,
+                               -16384 - 2097152 + 268435456, 128, 16384, 2097152};
+    long long prev[16], cc = 0;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) prev[c] = 0;
+    auto emit = [&](int w, long long v) {
+        if (w >= P2) return;
+        if (Cw) {
+            Cw[(size_t)w * nn + e] = v;
+        } else if (w < RL) {
+            const long long x = cc + v;
+            out[(size_t)w * nn + e] = (uint16_t)(x & 0xFFFF);
+            cc = x >> 16;
+        }
+    };
+#pragma unroll 1
+    for (int wb = 0; wb < NW; ++wb) {
+        long long cl[16], ch[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) cl[c] = ch[c] = 0;
+#pragma unroll
+        for (int m = 0; m < 6; ++m) {
+            const int32_t *p = P + mfh_c5_index(m * NW + wb, i, j, 0, np_, 1, 32, np_);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                typedef int v4i __attribute__((ext_vector_type(4)));
+                const v4i v4 = __builtin_nontemporal_load((const v4i *)(p + q * 64));
+                const int vv[4] = {v4[0], v4[1], v4[2], v4[3]};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 4 * q + r;
+                    if (t == 31) continue;
+                    const long long val =
+                        lo + (long long)(uint32_t)((uint32_t)vv[r] - (uint32_t)lo);
+                    if (t < 16) cl[t] += coef[m] * val;
+                    else ch[t - 16] += coef[m] * val;
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            emit(16 * wb + c, cl[c] + prev[c]);
+            prev[c] = ch[c];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 16; ++c) emit(16 * NW + c, prev[c]);
+    if (!Cw)
+        for (int w = P2; w < RL; ++w) {
+            out[(size_t)w * nn + e] = (uint16_t)(cc & 0xFFFF);
+            cc >>= 16;
+        }
+}
+
 }  // namespace
 
 int mfh_launch_entry_to_plane(const uint16_t *e, uint16_t *p, int n, int L, hipStream_t st)
@@ -217,6 +325,28 @@ int mfh_launch_conv_limbplane(int64_t *Cw, const void *A, const void *B, int in_
                            (const int32_t *)A, (const int32_t *)B, n, L, 0);
     else
         return MFH_E_ARG;
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_sb_digits(const void *src, int in_kind, int8_t *out, int n, int np_, int L,
+                         int NLp, hipStream_t st)
+{
+    const size_t threads = (size_t)NLp * np_ * np_ / 4;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (in_kind != MFH_IN_U16 && in_kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
+    hipLaunchKernelGGL(k_sb_digits<uint16_t>, grid, dim3(256), 0, st, (const uint16_t *)src, out,
+                       n, np_, L, NLp, (int)(in_kind == MFH_IN_U16_SIGNED));
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_sb_combine(const int32_t *P, int64_t *Cw, uint16_t *out, int RL, int n, int np_,
+                          int L, int NU, long long lo, hipStream_t st)
+{
+    const size_t nn = (size_t)n * n;
+    hipLaunchKernelGGL(k_sb_combine, dim3((unsigned)((nn + 255) / 256)), dim3(256), 0, st, P,
+                       (long long *)Cw, out, RL, n, np_, L, NU, lo);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }

@@ -1209,11 +1209,145 @@ int launch_gauss2(mfh_ctx *c, int rows)
     return MFH_OK;
 }
 
+// ============================================================================
+// Limb-plane schoolbook on the matrix cores (src/methods.c:94-104):
+//     Cw[w] = sum_{u+v=w} A_u B_v
+// with every limb split into the six int8 planes of its K7 digits (d0, d1,
+// d2 and the pair sums): for each Karatsuba class m the int8 planes q_m of
+// the limbs are convolved, Q_m[w] = sum_{u+v=w} q_m(A_u) q_m(B_v), and
+// Cw = sum_m coef_m Q_m (mfh_launch_sb_combine).  Limbs are taken in blocks
+// of 16: block pair (U, V) is a length-16 linear convolution of fragment
+// sequences (one sub-round of gs_sub, every diagonal d = c1 + c2 into
+// acc[d]), whose diagonals 0..15 fall on output block W = U + V and 16..30
+// on block W + 1.  A workgroup owns one 32 x 32 tile, one class m and one
+// W: it runs the block pairs (U, W - U) for every 64-wide k block and
+// stores its 31 diagonal sums as the partial P[m][W][d] (int32; exact
+// modulo 2^32, and the combine step knows each partial's range).
+// Sub-round s (pair U = Ulo + s / kblocks, k block s % kblocks) lives in
+// LDS slot s mod 2, with the two-barrier schedule of k_pointwise_gauss2.
+//
+// Digit planes (mfh_launch_sb_digits): [limb u < 16 NU][class plane][rows x
+// np in 16 x 64 tiles], A by rows, B transposed (entry (j', k) = B[k][j']).
+// P layout: mfh_c5_index with point m * NW + W, one class, K = 32.
+template <class Cfg>
+__global__ void __attribute__((amdgpu_flat_work_group_size(Cfg::THREADS, Cfg::THREADS),
+                               amdgpu_waves_per_eu(Cfg::WPE, Cfg::WPE)))
+k_schoolbook(const int8_t *__restrict__ Ad, const int8_t *__restrict__ Bd,
+             int32_t *__restrict__ P, int np_, int NU, int tiles_j)
+{
+    static_assert(Cfg::NSLOT == 2 && Cfg::H == 16 && Cfg::PRE > Cfg::BAR, "two-slot schedule");
+    constexpr int K = Cfg::K, H = Cfg::H, WBI = Cfg::WBI, WBJ = Cfg::WBJ, W = Cfg::WAVES;
+    constexpr int NA = Cfg::NA, NBF = Cfg::NBF, PL = 6;
+    __shared__ v4i sA0[Cfg::A_CHUNKS], sA1[Cfg::A_CHUNKS];
+    __shared__ v4i sB0[Cfg::B_CHUNKS], sB1[Cfg::B_CHUNKS];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wbi = wave / WBJ, wbj = wave % WBJ;
+    const int ti = blockIdx.x / tiles_j, tj = blockIdx.x % tiles_j;
+    const int NW = 2 * NU - 1;
+    const int Wb = blockIdx.y % NW, m = blockIdx.y / NW;
+    const int i0 = ti * Cfg::BI, j0 = tj * Cfg::BJ;
+    const size_t plane = (size_t)np_ * np_;
+    const int8_t *a_blk = Ad + ((size_t)(wave / WBI) * PL + m) * plane +
+                          mfh_tile_off(i0 + (wave % WBI) * 16, 0, np_) + (lane & 15) * 64 +
+                          (lane >> 4) * 16;
+    const int8_t *b_blk = Bd + ((size_t)(wave / WBJ) * PL + m) * plane +
+                          mfh_tile_off(j0 + (wave % WBJ) * 16, 0, np_) + (lane & 15) * 64 +
+                          (lane >> 4) * 16;
+    const size_t da = (size_t)(W / WBI) * PL * plane, db = (size_t)(W / WBJ) * PL * plane;
+    const int kblocks = np_ / MFH_KBLK;
+    const int Ulo = Wb - NU + 1 > 0 ? Wb - NU + 1 : 0, Uhi = Wb < NU - 1 ? Wb : NU - 1;
+    const int S = (Uhi - Ulo + 1) * kblocks;              // sub-rounds
+    // copies of sub-round s (s >= S: the last one again) into slot SL
+    auto copy = [&](auto stag, int s) {
+        constexpr int SL = decltype(stag)::value;
+        if (s >= S) s = S - 1;
+        const int U = Ulo + s / kblocks, kb = s % kblocks, V = Wb - U;
+        v4i *dA = SL == 0 ? sA0 : sA1;
+        v4i *dB = SL == 0 ? sB0 : sB1;
+        const int8_t *a0 = a_blk + (size_t)U * H * PL * plane + kb * 1024;
+        const int8_t *b0 = b_blk + (size_t)V * H * PL * plane + kb * 1024;
+#pragma unroll
+        for (int i = 0; i < NA; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(a0 + i * da),
+                                             (void *)(dA + (wave + i * W) * 64), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NBF; ++i)
+            __builtin_amdgcn_global_load_lds((const void *)(b0 + i * db),
+                                             (void *)(dB + (wave + i * W) * 64), 16, 0, 0);
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using G2 = std::integral_constant<int, 2>;
+    copy(S0{}, 0);
+    copy(S1{}, 1);
+    vm_lgkm_barrier<0>();
+    v4i acc[K], ng[H - 1];
+#pragma unroll
+    for (int t = 0; t < K; ++t) acc[t] = v4i{0, 0, 0, 0};
+    constexpr int D = Cfg::D;
+    v4i pa[D], pb[D];
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+        pa[c] = sA0[(c * WBI + wbi) * 64 + lane];
+        pb[c] = sB0[(c * WBJ + wbj) * 64 + lane];
+    }
+    // sub-round s in slot SL; its copies are those of sub-round s + 2
+    auto sub = [&](auto stag, int s) {
+        constexpr int SL = decltype(stag)::value;
+        const v4i *la = (SL == 0 ? sA0 : sA1) + wbi * 64 + lane;
+        const v4i *lb = (SL == 0 ? sB0 : sB1) + wbj * 64 + lane;
+        const v4i *nla = (SL == 0 ? sA1 : sA0) + wbi * 64 + lane;
+        const v4i *nlb = (SL == 0 ? sB1 : sB0) + wbj * 64 + lane;
+        gs_sub<Cfg, G2::value>(acc, ng, pa, pb, la, lb, nla, nlb, [&](int s0) {
+            if (s0 == Cfg::BAR) {
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                copy(stag, s + 2);
+            } else if (s0 == Cfg::PRE) {
+                vm_lgkm_wait6<Cfg::NPW>();
+                __builtin_amdgcn_s_barrier();
+            }
+        });
+    };
+#pragma unroll 1
+    for (int s = 0; s < S; s += 2) {
+        sub(S0{}, s);
+        if (s + 1 < S) sub(S1{}, s + 1);
+    }
+    const int col = j0 + wbj * 16 + (lane & 15);
+    const int row0 = i0 + wbi * 16 + 4 * (lane >> 4);
+    const int jp = m * NW + Wb;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+#pragma unroll
+        for (int tt = 0; tt < K; tt += 4) {
+            const v4i qv = {acc[tt][v], acc[tt + 1][v], acc[tt + 2][v],
+                            tt + 3 < K - 1 ? acc[tt + 3][v] : 0};
+            __builtin_nontemporal_store(
+                qv, (v4i *)(P + mfh_c5_index(jp, row0 + v, col, tt, np_, 1, K, np_)));
+        }
+    }
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));
+}
+
 }  // namespace
 
 // K values with a Gauss kernel (the forward transform writes Gauss slots
 // only for these)
 bool mfh_gauss_supported(int K) { return K == 16 || K == 32; }
+
+int mfh_launch_schoolbook(const int8_t *Ad, const int8_t *Bd, int32_t *P, int np_, int NU,
+                          hipStream_t st)
+{
+    using Cfg = GsCfg<32, 2, 2, 1, 4, 12, 24, false, 2>;
+    if (np_ % MFH_KBLK || np_ % Cfg::BI || np_ % Cfg::BJ || NU < 1) return MFH_E_ARG;
+    const int tiles_i = np_ / Cfg::BI, tiles_j = np_ / Cfg::BJ;
+    dim3 grid((unsigned)(tiles_i * tiles_j), (unsigned)(6 * (2 * NU - 1)));
+    hipLaunchKernelGGL(k_schoolbook<Cfg>, grid, dim3(Cfg::THREADS), 0, st, Ad, Bd, P, np_, NU,
+                       tiles_j);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
 
 int mfh_launch_pointwise(mfh_ctx *c, int rows)
 {

@@ -874,6 +874,89 @@ int mfh_limbplane_mm_dev(mfh_ctx *c, int in_kind, const void *dA, const void *dB
                                    (uint16_t *)dOut, RL, c ? c->stream : 0);
 }
 
+// ---- the limb-plane schoolbook on the matrix cores -------------------------
+namespace {
+struct SbLayout {
+    int np, NU;
+    size_t bt, digits, partials;     // bytes: B^T limbs, one operand's digits, P
+    long long lo;                    // lower end of every partial's range
+};
+// Every partial sums at most 16 NU digit products per k over n values of k,
+// each in [-128 * 127, 128 * 128]: its range has width 16 NU n 32640, which
+// must stay below 2^32 for the int32 residue to determine it.
+int sb_layout(int n, int L, SbLayout &s)
+{
+    if (n < 1 || L < 1) return MFH_E_ARG;
+    s.np = (n + MFH_KBLK - 1) / MFH_KBLK * MFH_KBLK;
+    s.NU = (L + 15) / 16;
+    const long long terms = 16LL * s.NU * n;
+    if (terms * 32640 >= (1LL << 32)) return MFH_E_BOUND;
+    s.lo = -terms * 16256;
+    const size_t plane = (size_t)s.np * s.np;
+    s.bt = ((size_t)L * n * n * 2 + 255) / 256 * 256;
+    s.digits = (size_t)16 * s.NU * 6 * plane;
+    s.partials = (size_t)6 * (2 * s.NU - 1) * plane * 32 * 4;
+    return MFH_OK;
+}
+}  // namespace
+
+int mfh_schoolbook_workspace(int n, int L, size_t *bytes)
+{
+    SbLayout s;
+    if (!bytes) return MFH_E_ARG;
+    const int rc = sb_layout(n, L, s);
+    if (rc) return rc;
+    *bytes = s.bt + 2 * s.digits + s.partials;
+    return MFH_OK;
+}
+
+int mfh_schoolbook_dev(mfh_ctx *c, int in_kind, const void *dA, const void *dB, int n, int L,
+                       void *dWork, size_t work_bytes, void *dOut, int RL)
+{
+    SbLayout s;
+    if (!dA || !dB || !dWork || !dOut || RL < 0) return MFH_E_ARG;
+    if (in_kind != MFH_IN_U16 && in_kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
+    int rc = sb_layout(n, L, s);
+    if (rc) return rc;
+    if (work_bytes < s.bt + 2 * s.digits + s.partials) return MFH_E_ARG;
+    hipStream_t st = c ? c->stream : 0;
+    char *w = (char *)dWork;
+    void *bt = w;
+    int8_t *ad = (int8_t *)(w + s.bt), *bd = ad + s.digits;
+    int32_t *P = (int32_t *)(bd + s.digits);
+    if ((rc = mfh_launch_transpose(dB, bt, L, n, 2, st)) ||
+        (rc = mfh_launch_sb_digits(dA, in_kind, ad, n, s.np, L, 16 * s.NU, st)) ||
+        (rc = mfh_launch_sb_digits(bt, in_kind, bd, n, s.np, L, 16 * s.NU, st)) ||
+        (rc = mfh_launch_schoolbook(ad, bd, P, s.np, s.NU, st)))
+        return rc;
+    return RL ? mfh_launch_sb_combine(P, nullptr, (uint16_t *)dOut, RL, n, s.np, L, s.NU, s.lo, st)
+              : mfh_launch_sb_combine(P, (int64_t *)dOut, nullptr, 0, n, s.np, L, s.NU, s.lo, st);
+}
+
+int mfh_schoolbook(int in_kind, const uint16_t *A, const uint16_t *B, int n, int L, void *out,
+                   int RL)
+{
+    if (!A || !B || !out || RL < 0) return MFH_E_ARG;
+    size_t work = 0;
+    int rc = mfh_schoolbook_workspace(n, L, &work);
+    if (rc) return rc;
+    if ((rc = check_device())) return rc;
+    const size_t nn = (size_t)n * n, in_b = (size_t)L * nn * 2;
+    const size_t out_b = RL ? (size_t)RL * nn * 2 : (size_t)(2 * L - 1) * nn * 8;
+    TmpBufs t;
+    if (hipMalloc(&t.p[0], 2 * in_b) != hipSuccess || hipMalloc(&t.p[1], work) != hipSuccess ||
+        hipMalloc(&t.p[2], out_b) != hipSuccess)
+        return MFH_E_NOMEM;
+    uint16_t *dA = (uint16_t *)t.p[0], *dB = dA + (size_t)L * nn;
+    MFH_HIP(hipMemcpy(dA, A, in_b, hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(dB, B, in_b, hipMemcpyHostToDevice));
+    if ((rc = mfh_schoolbook_dev(nullptr, in_kind, dA, dB, n, L, t.p[1], work, t.p[2], RL)))
+        return rc;
+    MFH_HIP(hipDeviceSynchronize());
+    MFH_HIP(hipMemcpy(out, t.p[2], out_b, hipMemcpyDeviceToHost));
+    return MFH_OK;
+}
+
 namespace {
 // conv_limbplane / mm_limbplane on host buffers: limb planes in, the 2L-1
 // coefficient planes (out == nullptr) or RL carried limbs out

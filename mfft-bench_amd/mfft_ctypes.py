@@ -92,6 +92,9 @@ def load(path=None):
         "mfh_limbplane_conv_dev": ([vp, i, vp, vp, i, i, vp], i),
         "mfh_limbplane_mm": ([vp, vp, i, i, vp, i], i),
         "mfh_limbplane_mm_dev": ([vp, i, vp, vp, i, i, vp, vp, i], i),
+        "mfh_schoolbook_workspace": ([i, i, C.POINTER(sz)], i),
+        "mfh_schoolbook_dev": ([vp, i, vp, vp, i, i, vp, sz, vp, i], i),
+        "mfh_schoolbook": ([i, vp, vp, i, i, vp, i], i),
         "mm_accum": ([vp, vp, vp, i, i, i], None),
         "mm_limbplane": ([vp, vp, i, i, i, vp, i], None),
         "conv_limbplane": ([vp, vp, vp, i, i, i], None),

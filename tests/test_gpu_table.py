@@ -27,12 +27,13 @@ def _rows(n, W, signed=False):
 
 @pytest.mark.parametrize("W", [128, 256, 512, 1024, 2048, 4096, 8192])
 def test_sweep_width_rows_exact(gpu, W):
-    """--sweep-width at n = 32: limbplane, mfft (and mfft-flatpw at K = 16)
-    and mfft-rec rows, all exact."""
+    """--sweep-width at n = 32: limbplane, limbplane-mma (the schoolbook on
+    the matrix cores), mfft (and mfft-flatpw at K = 16) and mfft-rec rows,
+    all exact."""
     print(f"[table] n=32 W={W}", flush=True)
     rows = _rows(32, W)
     names = [r[2] for r in rows]
-    assert names[0] == "limbplane" and "mfft" in names
+    assert names[:2] == ["limbplane", "limbplane-mma"] and "mfft" in names
     for r in rows:
         assert r[-1] == "yes", r
     mfft = next(r for r in rows if r[2] == "mfft")
