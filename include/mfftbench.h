@@ -95,8 +95,9 @@ void mm_bigint_ijk(const uint16_t *Aem, const uint16_t *Bem, int n, int L,
 void mm_bigint_ikj(const uint16_t *Aem, const uint16_t *Bem, int n, int L,
                    uint16_t *out, int RL);
 /* src/mfftbench.h:100-101: on the int8 matrix cores (mfh_schoolbook) where
- * the bound of its int32 partial sums holds (ceil(L/16) n <= 8224), else on
- * the integer ALU; exact either way */
+ * the bound of its int32 partial sums holds (ceil(L/16) n <= 8224) and its
+ * workspace fits in device memory, else on the integer ALU; exact either
+ * way */
 void mm_limbplane(const uint16_t *Apl, const uint16_t *Bpl, int n, int L,
                   kernel_t k, uint16_t *out, int RL);
 /* src/mfftbench.h:105-106 */

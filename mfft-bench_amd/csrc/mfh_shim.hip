@@ -945,8 +945,10 @@ int mfh_schoolbook(int in_kind, const uint16_t *A, const uint16_t *B, int n, int
     const size_t out_b = RL ? (size_t)RL * nn * 2 : (size_t)(2 * L - 1) * nn * 8;
     TmpBufs t;
     if (hipMalloc(&t.p[0], 2 * in_b) != hipSuccess || hipMalloc(&t.p[1], work) != hipSuccess ||
-        hipMalloc(&t.p[2], out_b) != hipSuccess)
+        hipMalloc(&t.p[2], out_b) != hipSuccess) {
+        (void)hipGetLastError();     // a caller may go on to a smaller method
         return MFH_E_NOMEM;
+    }
     uint16_t *dA = (uint16_t *)t.p[0], *dB = dA + (size_t)L * nn;
     MFH_HIP(hipMemcpy(dA, A, in_b, hipMemcpyHostToDevice));
     MFH_HIP(hipMemcpy(dB, B, in_b, hipMemcpyHostToDevice));

@@ -375,10 +375,11 @@ void mm_limbplane(const uint16_t *Apl, const uint16_t *Bpl, int n, int L, kernel
 {
     t_last_error = 0;
     if (k != KERNEL_HIP) { fail("mm_limbplane", MFH_E_UNSUPPORTED); return; }
-    /* on the matrix cores where their partial-sum bound holds, else on the
-     * integer ALU (both exact) */
+    /* on the matrix cores where their partial-sum bound holds and their
+     * workspace fits, else on the integer ALU (both exact; the ALU kernel
+     * needs only the 2L-1 int64 coefficient planes) */
     int rc = RL >= 1 ? mfh_schoolbook(MFH_IN_U16, Apl, Bpl, n, L, out, RL) : MFH_E_ARG;
-    if (rc == MFH_E_BOUND) rc = mfh_limbplane_mm(Apl, Bpl, n, L, out, RL);
+    if (rc == MFH_E_BOUND || rc == MFH_E_NOMEM) rc = mfh_limbplane_mm(Apl, Bpl, n, L, out, RL);
     if (rc) fail("mm_limbplane", rc);
 }
 
