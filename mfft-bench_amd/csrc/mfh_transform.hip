@@ -672,7 +672,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     constexpr int L = NB * S / 2;
     constexpr int TPE = 256 / E;
     static_assert(E * TPE == 256 && Q % TPE == 0, "threads split evenly over classes");
-    static_assert(XB == 0 || (XB < 3 && E == 256) || (XB == 3 && E == 64),
+    static_assert(XB == 0 || (XB < 3 && E == 256) || (XB == 3 && (E == 64 || E == 256)),
                   "staged stores: 256 elements per workgroup, or 64 per wave");
     __shared__ uint32_t xbuf[XB == 3 ? XCH_DWORDS : XB > 0 ? XB * XCH_DWORDS : 1];
     const size_t nnp = (size_t)rows * np_;           // the band's elements (plane stride)
@@ -1382,7 +1382,10 @@ bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_mode, int row0, int
 // (XB = 1): forward 2.04 -> 1.77 ms at W = 2048 (both operands and the B
 // transpose), 9.7 -> 6.2 ms at W = 512 and n = 4096, 1.71 -> 1.1 ms for
 // fp32 at n = 2048; two buffers (one barrier per chunk) measured equal or
-// slower.
+// slower.  Staging per wave with no workgroup barrier (XB = 3, 64-byte
+// runs per plane) pays only at W = 1024 (0.081 -> 0.071 ms at n = 64;
+// 2.53 -> 2.57 ms at W = 2048, n = 1024; 5.9 -> 7.9 ms at W = 512,
+// n = 4096).
 bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, int rows,
                       int gs)
 {
@@ -1395,7 +1398,7 @@ bool forward_fast_u16(mfh_ctx *c, const SrcU16 &s, int8_t *dst, int ts, int r0, 
                                                                        rows, gs) ||  // W=2048
            try_fast<8, 32, B8, false, SrcU16, LimbsLds<128>, 256, 8, 1>(c, s, dst, ts, r0, rows,
                                                                        gs) ||
-           try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>, 256, 4, 1>(c, s, dst, ts, r0,
+           try_fast<8, 16, K7, false, SrcU16, LimbsLds<64>, 256, 4, 3>(c, s, dst, ts, r0,
                                                                        rows, gs) ||  // W=1024
            try_fast<16, 64, K7, true, SrcU16, LimbsLds<512, 64>, 64, 32, 3>(c, s, dst, ts, r0,
                                                                            rows, gs) ||  // W=8192
