@@ -1334,7 +1334,7 @@ k_schoolbook(const int8_t *__restrict__ Ad, const int8_t *__restrict__ Bd,
 
 // K values with a Gauss kernel (the forward transform writes Gauss slots
 // only for these)
-bool mfh_gauss_supported(int K) { return K == 16 || K == 32; }
+bool mfh_gauss_supported(int K) { return K == 8 || K == 16 || K == 32; }
 
 int mfh_launch_schoolbook(const int8_t *Ad, const int8_t *Bd, int32_t *P, int np_, int NU,
                           hipStream_t st)
@@ -1359,6 +1359,12 @@ int mfh_launch_pointwise(mfh_ctx *c, int rows)
         // after diagonal group 4, the next sub-round's first pairs read
         // after group 8
         case 16: return launch_gauss<GsCfg<16, 4, 2, 2, 4, 4, 8, true>>(c, rows);
+        // 64 x 64 tiles, 16 waves at 4 per SIMD (96 KiB of slots), pairs
+        // read 3 ahead, barrier after diagonal group 2, the next
+        // sub-round's first pairs read after group 4 (512-bit n = 4096:
+        // pointwise 262.8 -> 245.0 ms, product 277.7 -> 263.0 ms; fp32 on
+        // the 512-bit grid at n = 2048 about equal)
+        case 8: return launch_gauss<GsCfg<8, 4, 4, 4, 3, 2, 4, false>>(c, rows);
         // 32 x 32 tiles, 4 waves at 1 per SIMD, two 64 KiB slots, pairs
         // read 4 ahead, slot refilled after diagonal group 12, the next
         // sub-round's copies waited for after group 24 (4.30 -> 4.18 ms

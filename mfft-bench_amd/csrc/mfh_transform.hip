@@ -309,12 +309,15 @@ __device__ __forceinline__ void xch_write(
         row[g * GSTRIDE] = pack4_lo(d[4 * g], d[4 * g + 1], d[4 * g + 2], d[4 * g + 3]);
 }
 
-// o: the first byte of the NE elements in the chunk's first plane
+// o: the first byte of the NE elements in the chunk's first plane; only
+// the first ngroups groups of 4 planes are stored (a point's last chunk may
+// be partial)
 template <int NE>
-__device__ __forceinline__ void xch_store(const uint32_t *buf, int8_t *o, size_t nnp, int t)
+__device__ __forceinline__ void xch_store(const uint32_t *buf, int8_t *o, size_t nnp, int t,
+                                          int ngroups = XCH_GROUPS)
 {
     constexpr int EB = NE / 16, GSTRIDE = EB * XCH_ROW;
-    if (t >= XCH_GROUPS * EB) return;
+    if (t >= ngroups * EB) return;
     const int g = t / EB, eb = t % EB;
     const uint4 *src = (const uint4 *)(buf + g * GSTRIDE + eb * XCH_ROW);
     uint32_t w[16];
@@ -581,19 +584,21 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
             // other lanes' reads above the writes, or the next chunk's writes
             // above this chunk's reads
             constexpr int CPC = XCH_PLANES / PL;
-            static_assert(NSL % CPC == 0, "whole chunks per point");
+            static_assert((NSL % CPC) * PL % 4 == 0, "whole groups of 4 planes per chunk");
             const int lane = threadIdx.x & 63;
             uint32_t *buf = xb + (threadIdx.x >> 6) * (XCH_DWORDS / 4);
             int8_t *wg = o - lane;
 #pragma unroll
             for (int c0 = 0; c0 < NSL; c0 += CPC) {
+                const int nv = NSL - c0 < CPC ? NSL - c0 : CPC;     // slots in this chunk
                 int zc[CPC];
 #pragma unroll
-                for (int c = 0; c < CPC; ++c) zc[c] = slot_val<GS, K>(z[pos], c0 + c);
+                for (int c = 0; c < CPC; ++c) zc[c] = c < nv ? slot_val<GS, K>(z[pos], c0 + c) : 0;
                 asm volatile("" ::: "memory");
                 xch_write<MODE, 64>(buf, zc, lane);
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                xch_store<64>(buf, wg + (size_t)((j * NSL + c0) * PL) * nnp, nnp, lane);
+                xch_store<64>(buf, wg + (size_t)((j * NSL + c0) * PL) * nnp, nnp, lane,
+                              nv * PL / 4);
             }
         } else {
             // chunks of CPC coefficients; chunk k of the kernel uses buffer
@@ -601,20 +606,22 @@ __device__ __forceinline__ void forward_class(const Limbs &x, int8_t *o, size_t 
             // chunk's readers are done) and one before the reads.  Two: the
             // barrier before the reads of chunk k also orders every read of
             // chunk k-1 before the writes of chunk k+1 into its buffer.
-            constexpr int CPC = XCH_PLANES / PL;
-            static_assert(NSL % CPC == 0, "whole chunks per point");
+            constexpr int CPC = XCH_PLANES / PL, NCH = (NSL + CPC - 1) / CPC;
+            static_assert((NSL % CPC) * PL % 4 == 0, "whole groups of 4 planes per chunk");
             int8_t *wg = o - threadIdx.x;
 #pragma unroll
             for (int c0 = 0; c0 < NSL; c0 += CPC) {
-                const int k = (q * P + pos) * (NSL / CPC) + c0 / CPC;
+                const int k = (q * P + pos) * NCH + c0 / CPC;
+                const int nv = NSL - c0 < CPC ? NSL - c0 : CPC;     // slots in this chunk
                 uint32_t *buf = xb + (k % XB) * XCH_DWORDS;
                 int zc[CPC];
 #pragma unroll
-                for (int c = 0; c < CPC; ++c) zc[c] = slot_val<GS, K>(z[pos], c0 + c);
+                for (int c = 0; c < CPC; ++c) zc[c] = c < nv ? slot_val<GS, K>(z[pos], c0 + c) : 0;
                 if (XB == 1 && k > 0) __syncthreads();
                 xch_write<MODE, 256>(buf, zc, threadIdx.x);
                 __syncthreads();
-                xch_store<256>(buf, wg + (size_t)((j * NSL + c0) * PL) * nnp, nnp, threadIdx.x);
+                xch_store<256>(buf, wg + (size_t)((j * NSL + c0) * PL) * nnp, nnp, threadIdx.x,
+                               nv * PL / 4);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1368,7 +1375,7 @@ bool try_fast(mfh_ctx *c, const Src &s, int8_t *dst, int top_mode, int row0, int
     if (gs == 0)
         return try_fast1<S, NB, MODE, RECODE, Src, Limbs, E, Q, XB, 0>(c, s, dst, top_mode,
                                                                          row0, rows);
-    if constexpr (MODE == MFH_MODE_K7 && (2 * S == 16 || 2 * S == 32)) {
+    if constexpr (MODE == MFH_MODE_K7 && (2 * S == 8 || 2 * S == 16 || 2 * S == 32)) {
         if (gs == 1)
             return try_fast1<S, NB, MODE, RECODE, Src, Limbs, E, Q, XB, 1>(c, s, dst, top_mode,
                                                                              row0, rows);

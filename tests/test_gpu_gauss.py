@@ -1,5 +1,6 @@
-"""The two pointwise algorithms at ring sizes K = 16 (W = 1024 and 2048 bits)
-and K = 32 (W = 4096 and 8192 bits, the two-slot kernel): the Gauss
+"""The two pointwise algorithms at ring sizes K = 8 (W = 512 bits), K = 16
+(W = 1024 and 2048 bits) and K = 32 (W = 4096 and 8192 bits, the two-slot
+kernel): the Gauss
 three-product split of the ring halves (the default there) and the
 K^2-product kernel (MFH_POINTWISE=flat, read at context creation) must give
 the same limbs, and both the oracle's.  Covers the exact track (unsigned and
@@ -27,6 +28,8 @@ def _ctx(gpu, monkeypatch, flat, n, L, p=None):
 @pytest.mark.parametrize("n,L,signed", [(8, 64, False), (64, 64, False), (100, 64, False),
                                         (24, 128, False), (7, 128, False), (130, 128, False),
                                         (40, 64, True), (72, 128, True),
+                                        (8, 32, False), (64, 32, False), (130, 32, False),
+                                        (33, 32, True),
                                         (8, 256, False), (64, 256, False), (33, 256, True),
                                         (16, 512, False), (72, 512, False), (40, 512, True)])
 def test_gauss_and_flat_products_agree(gpu, orc, monkeypatch, n, L, signed):
@@ -73,7 +76,7 @@ def test_gauss_row_bands_and_generic_kernels(gpu, orc, monkeypatch, n, L):
     monkeypatch.delenv("MFH_GENERIC_KERNELS")
 
 
-@pytest.mark.parametrize("n,L", [(9, 64), (33, 128), (20, 256)])
+@pytest.mark.parametrize("n,L", [(17, 32), (9, 64), (33, 128), (20, 256)])
 def test_gauss_conv_signed_limbs(gpu, orc, monkeypatch, n, L):
     """conv_mfft on signed limbs at the extremes: Gauss slot values reach the
     same bound as single coefficients."""
