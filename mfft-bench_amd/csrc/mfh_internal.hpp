@@ -152,9 +152,13 @@ struct mfh_ctx {
     int64_t *dCw;         // coefficient planes [2L-1][n][n]
     void *dBt;            // transposed B input, up to L*n*n int32
     int *dFlag;           // device error flags
-    // staging for host-buffer entry points (allocated on first use)
+    // staging for host-buffer entry points (allocated on first use), and two
+    // pinned host chunks the caller's memory is copied through (pin[b] is
+    // reusable once pev[b], recorded after its last transfer, has completed)
     void *dInA, *dInB, *dOut;
     size_t inBytes, outBytes;
+    void *pin[2];
+    hipEvent_t pev[2];
     size_t bytes;         // device bytes held
     // last product: output kind (0 limbs, 1 coefficient planes, 2 fp32),
     // output limbs, whether the carry ran inside the inverse kernel
