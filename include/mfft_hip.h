@@ -239,6 +239,44 @@ int mfh_bigint_mm(const uint16_t *Aem, const uint16_t *Bem, int n, int L, uint16
  * convolution folded by t^K = -1 */
 int mfh_negconv(const int32_t *A, const int32_t *B, int K, int n, int64_t *C);
 
+/* ---- multi-modular product ----------------------------------------------
+ * No counterpart in the reference: the same exact product as mfh_mm /
+ * mm_mfft (src/mfft.c:424-438) and mm_limbplane (src/methods.c:106-123),
+ * computed by residue number system arithmetic instead of the MFFT, for
+ * callers that want the product and not the transform.  The entries of A B
+ * are reduced modulo nm primes p <= 65279 whose product exceeds 4 n 2^(2W)
+ * (W = 16 L); per prime the product is four int8 GEMMs on the matrix cores,
+ * and the Chinese remainder theorem, one more int8 GEMM per element, gives
+ * the limbs.  Output as mfh_mm: RL >= 1 uint16 limb planes of the product
+ * modulo 2^(16 RL) (two's complement for MFH_IN_U16_SIGNED), the limbs above
+ * 2L+1 the sign extension.  Limits: n <= 32768, L <= 512 (MFH_E_BOUND). */
+typedef struct mfh_rns mfh_rns;
+/* plan only (host): the number of primes for n x n matrices of L limbs, the
+ * first min(cap, count) of them (descending) written to primes */
+int  mfh_rns_primes(int n, int L, int *primes, int cap);
+int  mfh_rns_create(mfh_rns **ctx, int n, int L);
+void mfh_rns_destroy(mfh_rns *ctx);
+/* primes, padded size np (a multiple of 128), device bytes held */
+int  mfh_rns_info(const mfh_rns *ctx, int *nprimes, int *np, size_t *bytes);
+int  mfh_rns_mm_dev(mfh_rns *ctx, int in_kind, const void *dA, const void *dB, void *dOut,
+                    int RL);
+int  mfh_rns_mm(mfh_rns *ctx, int in_kind, const uint16_t *A, const uint16_t *B, uint16_t *out,
+                int RL);
+/* the residues of one operand read as rows r, inner index k (A, or B
+ * transposed): dR gets nprimes planes of np x np uint16 digit pairs
+ * lo | hi << 8 (r mod p = 256 (int8)hi + (int8)lo, |r| <= (p-1)/2), zero
+ * outside n x n (a stage of mfh_rns_mm_dev, for tests) */
+int  mfh_rns_residues_dev(mfh_rns *ctx, int in_kind, const void *dX, void *dR);
+int  mfh_rns_sync(mfh_rns *ctx);
+/* stage times of the most recent product while timing is on: [0] B
+ * transposed and the residues of both operands, [1] the per-prime GEMMs,
+ * [2] CRT and carry, [3] total */
+int  mfh_rns_set_timing(mfh_rns *ctx, int enable);
+int  mfh_rns_stage_times(const mfh_rns *ctx, float ms[4]);
+/* int8 MFMA ops the three stages issue (over the padded size np) */
+int  mfh_rns_work(const mfh_rns *ctx, double *residue_ops, double *pointwise_ops,
+                  double *crt_ops);
+
 /* ---- device memory and timing helpers ----------------------------------- */
 int  mfh_malloc(void **dptr, size_t bytes);
 int  mfh_free(void *dptr);

@@ -1,0 +1,904 @@
+// mfh_rns.hip -- exact product of big-integer matrices by multi-modular
+// (residue number system) arithmetic on the gfx950 int8 matrix cores.
+//
+// No counterpart in the reference: it computes the same function as
+// mm_mfft / mm_limbplane (src/mfft.c:424-438, src/methods.c:106-123) -- the
+// exact product of two n x n matrices of W = 16 L-bit integers, carried into
+// RL uint16 limbs modulo 2^(16 RL) -- by another algorithm.  The MFFT issues
+// NB K^2 small-integer GEMMs, about 8 L S of them (S ~ sqrt(L/2)); residues
+// modulo 16-bit primes need about 2 (2W + log2 n) / 16 primes of 4 int8
+// GEMMs each, linear in W.
+//
+// An entry of A B has at most 2W + log2(n) bits.  It is fixed by its
+// residues modulo nm distinct primes p_m <= 65279 whose product M exceeds
+// 4 n 2^(2W) (so |C| <= M/4 for unsigned and two's complement entries):
+//   1. residues (k_rns_residue): an entry with bytes b_t (t < 2L) is
+//        x = sum_t b_t 256^t  [- 2^W if it is a negative two's complement],
+//      so x = sum_t (b_t - 128) w_{m,t} + 128 sum_t w_{m,t} [- 2^W]
+//      (mod p_m) with w_{m,t} = 256^t mod p_m: an int8 GEMM of the shifted
+//      bytes against the two balanced base-2^8 digits of the weights (two
+//      int32 sums per prime, |sum| <= 2L 2^14), then reduced exactly in fp64.
+//      A residue r is kept balanced, |r| <= (p-1)/2 <= 32639, as its two
+//      balanced base-2^8 digits lo = ((r+128) & 255) - 128,
+//      hi = (r - lo)/256, both int8: the uint16 "digit pair" lo | hi << 8;
+//   2. pointwise (k_rns_pointwise): per prime, C_m = A_m B_m over the digit
+//      pairs: four int8 GEMMs into three int32 classes hh, hl + lh, ll
+//      (|class| <= 2 n 2^14), recombined exactly in fp64 as
+//      65536 hh + 256 (hl+lh) + ll, reduced mod p_m, multiplied by
+//      cinv_m = (M/p_m)^-1 mod p_m and reduced again: y_m, a digit pair;
+//   3. CRT (k_rns_crt): C = sum_m y_m M/p_m - q M, q = round(sum_m y_m/p_m)
+//      (exact: the fp64 sum errs by far less than the 1/4 margin).  The sum
+//      is an int8 GEMM of the y digits against the balanced base-2^8 digits
+//      of M/p_m (for lo) and of 256 M/p_m (for hi), one int32 column per
+//      output byte (|column| <= 2 nm 2^14); q times the digits of M is
+//      subtracted per column, groups of four columns are combined into int64
+//      values of weight 2^(32 g), and the groups are carried into RL uint16
+//      limbs by carry lookahead.  Everything is computed modulo
+//      256^Jpad, Jpad >= 2 (2L+1) bytes: the RL <= 2L+1 output limbs are
+//      exact; limbs beyond 2L+1 are the sign extension.
+//
+// MFMA: v_mfma_i32_16x16x64_i8.  Operand fragments: lane l holds row l%16 and
+// 16 k bytes 16 (l/16) .. +15 (A and B use the same k order); results: lane
+// l, value v is row 4 (l/16) + v, column l%16.
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "mfh_internal.hpp"
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// per prime: p, the residue offsets k0 = 128 sum_t w_t and k1 = k0 - 2^W
+// (mod p, in [0, p)), cinv = (M/p)^-1 mod p, and 1/p
+struct RnsMod {
+    int p, k0, k1, cinv;
+    double invp;
+};
+static_assert(sizeof(RnsMod) == 24, "RnsMod layout");
+
+constexpr int kPrimeMax = 65279;   // (p-1)/2 <= 32639 keeps the hi digit in int8
+constexpr int kPrimeMin = 16411;   // smallest prime the plans draw on
+
+// balanced residue of an exact integer value held in a double (|v| < 2^53)
+__device__ __forceinline__ int rns_reduce(double v, int p, double invp)
+{
+    const double q = rint(v * invp);
+    int r = (int)fma(-q, (double)p, v);            // exact: the result is small
+    const int h = p >> 1;
+    if (r > h) r -= p;
+    else if (r < -h) r += p;
+    return r;
+}
+
+// digit pair of a balanced residue, |r| <= 32639
+__device__ __forceinline__ uint16_t rns_pair(int r)
+{
+    const int lo = ((r + 128) & 255) - 128;
+    const int hi = (r - lo) >> 8;
+    return (uint16_t)((lo & 255) | ((hi & 255) << 8));
+}
+
+__device__ __forceinline__ int rns_unpair(uint16_t w)
+{
+    return (int)(int8_t)(w >> 8) * 256 + (int)(int8_t)(w & 255);
+}
+
+// s_waitcnt vmcnt(V) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+template <int V>
+__device__ __forceinline__ void wait_vm_lgkm()
+{
+    __builtin_amdgcn_s_waitcnt((V & 15) | (7 << 4) | (0 << 8) | ((V >> 4) << 14));
+}
+
+// ---- 1. residues -----------------------------------------------------------
+// X: L uint16 limb planes of an n x n matrix (plane u at X + u n^2), read as
+// the GEMM operand "rows r, inner index k" (A, or B^T).  R: nm digit-pair
+// planes of np x np (row stride np), zero outside n x n.  A wave owns EB
+// blocks of 16 consecutive k of row r = blockIdx.y and keeps their byte
+// fragments of all KB 64-byte k blocks in registers; W holds the weight
+// fragments [nm/8][KB][64 lanes][16 B]: fragment (ob, kb) row o = 16 ob + l%16
+// is digit o%2 (0: lo, 1: hi) of w_{8 ob + o/2, t}, t = 64 kb + byte.
+template <int KB, int EB>
+__global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict__ X, int n,
+                                                     int np_, int L, int sgn,
+                                                     const v4i *__restrict__ W,
+                                                     const RnsMod *__restrict__ mods, int nm,
+                                                     uint16_t *__restrict__ R)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int r = blockIdx.y;
+    const int k0 = (blockIdx.x * 4 + wave) * 16 * EB;
+    if (k0 >= np_) return;
+    const size_t nn = (size_t)n * n, npp = (size_t)np_ * np_;
+    v4i ef[KB][EB];
+    int sb[EB];
+    bool ok[EB];
+#pragma unroll
+    for (int cb = 0; cb < EB; ++cb) {
+        const int k = k0 + 16 * cb + col;
+        ok[cb] = r < n && k < n;
+        const uint16_t *base = X + (ok[cb] ? (size_t)r * n + k : 0);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            uint32_t d[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int u = 32 * kb + 8 * grp + 2 * q;
+                const uint32_t x0 = (ok[cb] && u < L) ? base[(size_t)u * nn] : 0;
+                const uint32_t x1 = (ok[cb] && u + 1 < L) ? base[(size_t)(u + 1) * nn] : 0;
+                d[q] = (x0 | (x1 << 16)) ^ 0x80808080u;      // bytes b - 128
+            }
+            ef[kb][cb] = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+        }
+        sb[cb] = (sgn && ok[cb]) ? (base[(size_t)(L - 1) * nn] >> 15) : 0;
+    }
+#pragma unroll 1
+    for (int ob = 0; ob < nm / 8; ++ob) {
+        v4i acc[EB];
+#pragma unroll
+        for (int cb = 0; cb < EB; ++cb) acc[cb] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            const v4i w = W[((size_t)ob * KB + kb) * 64 + lane];
+#pragma unroll
+            for (int cb = 0; cb < EB; ++cb)
+                acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, ef[kb][cb], acc[cb], 0, 0, 0);
+        }
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+            const int m = 8 * ob + 2 * grp + mm;
+            const RnsMod md = mods[m];
+            uint16_t *dst = R + (size_t)m * npp + (size_t)r * np_;
+#pragma unroll
+            for (int cb = 0; cb < EB; ++cb) {
+                const int k = k0 + 16 * cb + col;
+                if (k >= np_) continue;
+                uint16_t w = 0;
+                if (ok[cb]) {
+                    const double v = (double)acc[cb][2 * mm + 1] * 256.0 +
+                                     (double)acc[cb][2 * mm] + (double)(sb[cb] ? md.k1 : md.k0);
+                    w = rns_pair(rns_reduce(v, md.p, md.invp));
+                }
+                dst[k] = w;
+            }
+        }
+    }
+}
+
+// ---- 2. pointwise ----------------------------------------------------------
+// Per prime m: the 128 x 128 output tile (ti, tj) of A_m B_m^T over the
+// digit pairs (RA rows i, RB rows j, both k-contiguous, np x np), four
+// waves of 64 x 64.  k blocks of 64 reach LDS by buffer-to-LDS copies, three
+// stages deep (each stage its own array, so that the compiler does not wait
+// for copies into one stage before reading another).  Stage layout per
+// operand: 8 blocks of 16 rows; a block is 128 16-byte chunks, chunk
+// (2 kq + h) 16 + r holding words 16 kq + 8 h .. +7 of row r, so lane l of a
+// fragment reads chunks 32 (l/16) + l%16 and 32 (l/16) + 16 + l%16.
+struct PwStage {
+    v4i a[8][128];
+    v4i b[8][128];
+};
+
+__device__ __forceinline__ void rns_issue(PwStage &st, const char *a0, const char *b0,
+                                          size_t rowb, int kb, int wave, const uint32_t off[2])
+{
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii) {
+        const int idx = wave + 4 * ii;               // 0..31
+        const int opnd = idx >> 4, rb = (idx & 15) >> 1, sh = idx & 1;
+        const char *src = (opnd ? b0 : a0) + (size_t)16 * rb * rowb + (size_t)kb * 128 + off[sh];
+        v4i *dst = opnd ? &st.b[rb][64 * sh] : &st.a[rb][64 * sh];
+        __builtin_amdgcn_global_load_lds((const void *)src, (void *)dst, 16, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void rns_split(const v4i d0, const v4i d1, v4i &lo, v4i &hi)
+{
+    // d0: words 0..7 (2 per dword), d1: words 8..15; word = lo byte | hi byte << 8
+    lo = v4i{(int)__builtin_amdgcn_perm((uint32_t)d0.y, (uint32_t)d0.x, 0x06040200u),
+             (int)__builtin_amdgcn_perm((uint32_t)d0.w, (uint32_t)d0.z, 0x06040200u),
+             (int)__builtin_amdgcn_perm((uint32_t)d1.y, (uint32_t)d1.x, 0x06040200u),
+             (int)__builtin_amdgcn_perm((uint32_t)d1.w, (uint32_t)d1.z, 0x06040200u)};
+    hi = v4i{(int)__builtin_amdgcn_perm((uint32_t)d0.y, (uint32_t)d0.x, 0x07050301u),
+             (int)__builtin_amdgcn_perm((uint32_t)d0.w, (uint32_t)d0.z, 0x07050301u),
+             (int)__builtin_amdgcn_perm((uint32_t)d1.y, (uint32_t)d1.x, 0x07050301u),
+             (int)__builtin_amdgcn_perm((uint32_t)d1.w, (uint32_t)d1.z, 0x07050301u)};
+}
+
+struct PwAcc {
+    v4i hh[4][4], md[4][4], ll[4][4];
+};
+
+__device__ __forceinline__ void rns_compute(const PwStage &st, int wi, int wj, int lane,
+                                            PwAcc &c)
+{
+    const int c0 = 32 * (lane >> 4) + (lane & 15);
+    v4i alo[4], ahi[4], blo[4], bhi[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) rns_split(st.a[4 * wi + a][c0], st.a[4 * wi + a][c0 + 16], alo[a], ahi[a]);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) rns_split(st.b[4 * wj + b][c0], st.b[4 * wj + b][c0 + 16], blo[b], bhi[b]);
+    // dependent MFMAs into md are 16 issues apart
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            c.hh[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[a], bhi[b], c.hh[a][b], 0, 0, 0);
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            c.md[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[a], blo[b], c.md[a][b], 0, 0, 0);
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            c.ll[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[a], blo[b], c.ll[a][b], 0, 0, 0);
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            c.md[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[a], bhi[b], c.md[a][b], 0, 0, 0);
+}
+
+// Workgroup b -> (prime, tile): workgroup b runs on XCD b mod 8; XCD x takes
+// the primes m = x (mod 8), all tiles of one prime after another, so the
+// ~32 workgroups resident on an XCD share one prime's operand panels.
+__global__ __launch_bounds__(256) void k_rns_pointwise(const uint16_t *__restrict__ RA,
+                                                       const uint16_t *__restrict__ RB,
+                                                       const RnsMod *__restrict__ mods, int nm,
+                                                       int np_, uint16_t *__restrict__ Y)
+{
+    __shared__ PwStage s0, s1, s2;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wi = wave >> 1, wj = wave & 1;
+    const int tpr = np_ / 128, T = tpr * tpr;
+    const int bid = blockIdx.x, xcd = bid & 7, loc = bid >> 3;
+    const int m = (loc / T) * 8 + xcd, tile = loc % T;
+    if (m >= nm) return;
+    const int ti = tile / tpr, tj = tile % tpr;
+    const size_t npp = (size_t)np_ * np_, rowb = (size_t)np_ * 2;
+    const char *a0 = (const char *)(RA + m * npp + (size_t)ti * 128 * np_);
+    const char *b0 = (const char *)(RB + m * npp + (size_t)tj * 128 * np_);
+    uint32_t off[2];
+#pragma unroll
+    for (int sh = 0; sh < 2; ++sh) {
+        const int c = 64 * sh + lane;
+        off[sh] = (uint32_t)((c & 15) * rowb + (16 * (c >> 5) + 8 * ((c >> 4) & 1)) * 2);
+    }
+    PwAcc acc;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc.hh[a][b] = acc.md[a][b] = acc.ll[a][b] = v4i{0, 0, 0, 0};
+    const int nkb = np_ / 64;
+    rns_issue(s0, a0, b0, rowb, 0, wave, off);
+    if (nkb > 1) rns_issue(s1, a0, b0, rowb, 1, wave, off);
+    // Stage kb % 3 is complete once this wave's copies of kb are (only those
+    // of kb + 1 may remain: 8 per wave) and every wave has passed the
+    // barrier; the barrier also retires every read of stage (kb + 2) % 3
+    // (block kb - 1), which the copies of kb + 2 then overwrite.
+#define RNS_STEP(S, SN, KB)                                                   \
+    {                                                                         \
+        if ((KB) + 1 < nkb) wait_vm_lgkm<8>(); else wait_vm_lgkm<0>();        \
+        __builtin_amdgcn_s_barrier();                                         \
+        if ((KB) + 2 < nkb) rns_issue(SN, a0, b0, rowb, (KB) + 2, wave, off); \
+        rns_compute(S, wi, wj, lane, acc);                                    \
+    }
+    // no exits inside the unrolled body: with them the accumulators were
+    // copied at every exit and spilled
+    int kb = 0;
+#pragma unroll 1
+    for (; kb + 3 <= nkb; kb += 3) {
+        RNS_STEP(s0, s2, kb)
+        RNS_STEP(s1, s0, kb + 1)
+        RNS_STEP(s2, s1, kb + 2)
+    }
+    if (kb < nkb) RNS_STEP(s0, s2, kb)
+    if (kb + 1 < nkb) RNS_STEP(s1, s0, kb + 1)
+#undef RNS_STEP
+    const RnsMod md = mods[m];
+    uint16_t *y = Y + m * npp;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int i = ti * 128 + 64 * wi + 16 * a + 4 * (lane >> 4) + v;
+                const int j = tj * 128 + 64 * wj + 16 * b + (lane & 15);
+                const double cv = (double)acc.hh[a][b][v] * 65536.0 +
+                                  (double)acc.md[a][b][v] * 256.0 + (double)acc.ll[a][b][v];
+                const int c = rns_reduce(cv, md.p, md.invp);
+                const int yv = rns_reduce((double)c * (double)md.cinv, md.p, md.invp);
+                y[(size_t)i * np_ + j] = rns_pair(yv);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+}
+
+// ---- 3. CRT and carry ------------------------------------------------------
+// E = 16 EB elements (row i = blockIdx.y, columns j0 .. j0+E-1) per
+// workgroup.  LDS: the y digit pairs of the E elements as MFMA B fragments
+// [KBc][EB][64 lanes][16 B] (fragment (kb, cb): element 16 cb + l%16, the
+// digit pairs of primes 32 kb + 8 (l/16) .. +7), the int64 groups
+// [G = Jpad/4][E], and the carry lookahead's run data.  T holds the A
+// fragments [Jpad/16][KBc][64][16 B]: row j (output byte) of k = 2m + d is
+// byte j of M/p_m (d = 0) or of 256 M/p_m (d = 1), zero for m >= nm.
+template <int EB>
+__global__ __launch_bounds__(256) void k_rns_crt(const uint16_t *__restrict__ Y, int n, int np_,
+                                                 int nm, int KBc, int Jpad,
+                                                 const v4i *__restrict__ T,
+                                                 const int8_t *__restrict__ mb,
+                                                 const RnsMod *__restrict__ mods,
+                                                 uint16_t *__restrict__ out, int RL, int RLc)
+{
+    constexpr int E = 16 * EB, SEGS = 256 / E;
+    extern __shared__ __align__(16) unsigned char smem[];
+    v4i *yl = (v4i *)smem;                                        // KBc*EB*64
+    long long *grp = (long long *)(yl + (size_t)KBc * EB * 64);  // [G][E]
+    const int G = Jpad / 4;
+    double *qs = (double *)(grp + (size_t)G * E);                 // [256]
+    long long *segc = (long long *)(qs + 256);                    // [SEGS][E] x 4
+    long long *seglo = segc + 256, *seghi = seglo + 256, *segin = seghi + 256;
+    int *qv = (int *)(segin + 256);                               // [E]
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int i = blockIdx.y, j0 = blockIdx.x * E;
+    const size_t npp = (size_t)np_ * np_, nn = (size_t)n * n;
+
+    // 1. y digit pairs into LDS, and the partial sums of y_m / p_m
+    {
+        const int e = tid % E, mg = tid / E;
+        const bool ev = j0 + e < n;
+        const uint16_t *src = Y + (size_t)i * np_ + j0 + e;
+        uint16_t *yw = (uint16_t *)yl;
+        double qsum = 0;
+        for (int m = mg; m < 32 * KBc; m += SEGS) {
+            uint16_t w = 0;
+            if (m < nm && ev) {
+                w = src[(size_t)m * npp];
+                qsum += (double)rns_unpair(w) * mods[m].invp;
+            }
+            const int kb = m >> 5, mq = m & 31;
+            const int ln = (e & 15) + 16 * (mq >> 3);
+            yw[(((size_t)kb * EB + (e >> 4)) * 64 + ln) * 8 + (mq & 7)] = w;
+        }
+        qs[tid] = qsum;
+    }
+    __syncthreads();
+    if (tid < E) {
+        double s = 0;
+        for (int r = 0; r < SEGS; ++r) s += qs[r * E + tid];
+        qv[tid] = (int)rint(s);
+    }
+    __syncthreads();
+
+    // 2. byte columns: GEMM over the y digits, q M subtracted, groups of 4
+    const int nch = Jpad / 64;
+    for (int ch = wave; ch < nch; ch += 4) {
+        v4i acc[4][EB];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+            for (int cb = 0; cb < EB; ++cb) acc[jj][cb] = v4i{0, 0, 0, 0};
+        const v4i *tp = T + (size_t)4 * ch * KBc * 64 + lane;
+        v4i tf[4], tn[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) tf[jj] = tp[(size_t)jj * KBc * 64];
+#pragma unroll 1
+        for (int kb = 0; kb < KBc; ++kb) {
+            if (kb + 1 < KBc) {
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) tn[jj] = tp[((size_t)jj * KBc + kb + 1) * 64];
+            }
+            v4i yf[EB];
+#pragma unroll
+            for (int cb = 0; cb < EB; ++cb) yf[cb] = yl[((size_t)kb * EB + cb) * 64 + lane];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                for (int cb = 0; cb < EB; ++cb)
+                    acc[jj][cb] =
+                        __builtin_amdgcn_mfma_i32_16x16x64_i8(tf[jj], yf[cb], acc[jj][cb], 0, 0, 0);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) tf[jj] = tn[jj];
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+            for (int cb = 0; cb < EB; ++cb) {
+                const int el = 16 * cb + (lane & 15);
+                const int gi = 4 * (4 * ch + jj) + (lane >> 4);
+                const long long q = qv[el];
+                long long g = 0;
+#pragma unroll
+                for (int v = 3; v >= 0; --v)
+                    g = g * 256 + ((long long)acc[jj][cb][v] - q * (long long)mb[4 * gi + v]);
+                grp[(size_t)gi * E + el] = g;
+            }
+    }
+    __syncthreads();
+
+    // 3. carry lookahead over the Gc groups that hold the RLc output limbs:
+    // SEGS runs of len >= 2 groups per element.  A run propagates with
+    // carry-in 0 (its 32-bit words Ls, carry-out c); with the true carry-in
+    // X (|X| < 2^40) its carry-out is c + 1 when X >= 2^(32 len) - Ls,
+    // c - 1 when X < -Ls, else c.  Ls's low 64 bits and whether its higher
+    // words are all 0 or all 1 give both thresholds whenever they are
+    // representable; otherwise the case cannot occur.  The last run's
+    // carry-out is discarded (it lies above the output).
+    const int Gc = (RLc + 1) / 2;
+    int len = (Gc + SEGS - 1) / SEGS;
+    if (len < 2) len = 2;
+    const int el = tid % E, sg = tid / E;
+    const int g0 = sg * len, g1 = min(g0 + len, Gc);
+    {
+        long long cc = 0;
+        uint64_t low = 0;
+        bool zero_hi = true, ones_hi = true;
+        for (int g = g0; g < g1; ++g) {
+            const long long v = cc + grp[(size_t)g * E + el];
+            const uint64_t w = (uint64_t)v & 0xFFFFFFFFull;
+            const int ix = g - g0;
+            if (ix < 2) low |= w << (32 * ix);
+            else {
+                zero_hi &= w == 0;
+                ones_hi &= w == 0xFFFFFFFFull;
+            }
+            cc = v >> 32;
+        }
+        const bool top_clear = (low >> 63) == 0;
+        seglo[sg * E + el] = (zero_hi && top_clear) ? -(long long)low : INT64_MIN;
+        seghi[sg * E + el] =
+            (ones_hi && !top_clear && low != (1ull << 63)) ? (long long)(0 - low) : INT64_MAX;
+        segc[sg * E + el] = cc;
+    }
+    __syncthreads();
+    if (tid < E) {
+        long long C = 0;
+        for (int r = 0; r < SEGS; ++r) {
+            segin[r * E + tid] = C;
+            C = segc[r * E + tid] + (C >= seghi[r * E + tid]) - (C < seglo[r * E + tid]);
+        }
+    }
+    __syncthreads();
+    if (j0 + el < n) {
+        long long cc = segin[sg * E + el];
+        uint16_t *o = out + (size_t)i * n + j0 + el;
+        uint32_t top = 0;
+        for (int g = g0; g < g1; ++g) {
+            const long long v = cc + grp[(size_t)g * E + el];
+            const uint32_t w = (uint32_t)v;
+            const int u = 2 * g;
+            o[(size_t)u * nn] = (uint16_t)w;
+            top = w & 0xFFFF;
+            if (u + 1 < RLc) {
+                o[(size_t)(u + 1) * nn] = (uint16_t)(w >> 16);
+                top = w >> 16;
+            }
+            cc = v >> 32;
+        }
+        // limbs above 2L+1: the sign extension of limb RLc-1
+        if (g1 == Gc && g0 < g1 && RL > RLc) {
+            const uint16_t ext = (top & 0x8000) ? 0xFFFF : 0;
+            for (int u = RLc; u < RL; ++u) o[(size_t)u * nn] = ext;
+        }
+    }
+}
+
+size_t crt_lds_bytes(int EB, int KBc, int Jpad)
+{
+    const int E = 16 * EB;
+    return (size_t)KBc * EB * 1024 + (size_t)(Jpad / 4) * E * 8 + 256 * 8 + 4 * 256 * 8 + E * 4;
+}
+
+// ---- host planning ---------------------------------------------------------
+// primes in [kPrimeMin, kPrimeMax], descending
+const std::vector<int> &prime_list()
+{
+    static std::vector<int> pr;
+    if (pr.empty()) {
+        std::vector<char> comp(kPrimeMax + 1, 0);
+        for (int a = 2; (long long)a * a <= kPrimeMax; ++a)
+            if (!comp[a])
+                for (int b = a * a; b <= kPrimeMax; b += a) comp[b] = 1;
+        for (int p = kPrimeMax; p >= kPrimeMin; --p)
+            if (!comp[p]) pr.push_back(p);
+    }
+    return pr;
+}
+
+// the primes of a plan: the largest ones until sum log2 p >= 2W + ceil(log2 n)
+// + 3 (M > 4 n 2^(2W) with a bit to spare), then up to a multiple of 8
+int plan_primes(int n, int L, std::vector<int> &ps)
+{
+    ps.clear();
+    int lg = 0;
+    while ((1LL << lg) < n) ++lg;
+    const double need = 2.0 * 16 * L + lg + 3;
+    const std::vector<int> &pr = prime_list();
+    double bits = 0;
+    size_t k = 0;
+    while (k < pr.size() && (bits < need || ps.size() % 8)) {
+        ps.push_back(pr[k]);
+        bits += log2((double)pr[k]);
+        ++k;
+    }
+    if (bits < need || ps.size() % 8) return MFH_E_BOUND;
+    return MFH_OK;
+}
+
+long long modinv(long long a, long long p)
+{
+    long long t = 0, nt = 1, r = p, nr = ((a % p) + p) % p;
+    while (nr) {
+        const long long q = r / nr;
+        long long x = t - q * nt; t = nt; nt = x;
+        x = r - q * nr; r = nr; nr = x;
+    }
+    return t < 0 ? t + p : t;
+}
+
+// balanced base-256 digits d_j (j < J) of a non-negative integer held as
+// little-endian 32-bit words: sum_j d_j 256^j = value mod 256^J
+void balanced_bytes(const std::vector<uint32_t> &v, int J, int8_t *d)
+{
+    int carry = 0;
+    for (int j = 0; j < J; ++j) {
+        const size_t w = (size_t)j / 4;
+        int b = w < v.size() ? (int)((v[w] >> (8 * (j % 4))) & 255) : 0;
+        b += carry;
+        if (b >= 128) { b -= 256; carry = 1; } else carry = 0;
+        d[j] = (int8_t)b;
+    }
+}
+
+int kres_blocks(int L)
+{
+    const int kb = (2 * L + 63) / 64;
+    int b = 1;
+    while (b < kb) b *= 2;
+    return b;
+}
+
+}  // namespace
+
+struct mfh_rns {
+    int n, np, L, nm, nmk, KB, Jpad, crt_eb;
+    int dev;
+    hipStream_t stream;
+    RnsMod *dMod;
+    v4i *dW, *dT;
+    int8_t *dMb;
+    uint16_t *dRA, *dRB, *dY, *dBt;
+    size_t bytes;
+    int timing;
+    hipEvent_t ev[4];
+    std::vector<int> primes;
+};
+
+namespace {
+
+int rns_alloc(mfh_rns *r, void **p, size_t bytes)
+{
+    *p = nullptr;
+    if (!bytes) return MFH_OK;
+    if (hipMalloc(p, bytes) != hipSuccess) { *p = nullptr; return MFH_E_NOMEM; }
+    r->bytes += bytes;
+    return MFH_OK;
+}
+
+// weight fragments of the residue GEMM and the CRT tables
+int rns_tables(mfh_rns *r)
+{
+    const int nm = r->nm, L = r->L, KB = r->KB, Jpad = r->Jpad, nmk = r->nmk;
+    const int KBc = nmk / 32;
+    std::vector<RnsMod> mods(nm);
+    // residue weights: [nm/8][KB][64][16]
+    std::vector<int8_t> W((size_t)(nm / 8) * KB * 1024, 0);
+    std::vector<int8_t> wlo((size_t)2 * L), whi((size_t)2 * L);
+    for (int m = 0; m < nm; ++m) {
+        const long long p = r->primes[m];
+        long long w = 1, s1 = 0;
+        for (int t = 0; t < 2 * L; ++t) {
+            const long long wb = w > p / 2 ? w - p : w;
+            const long long lo = ((wb + 128) & 255) - 128;
+            wlo[t] = (int8_t)lo;
+            whi[t] = (int8_t)((wb - lo) / 256);
+            s1 = (s1 + w) % p;
+            w = w * 256 % p;
+        }
+        const long long k0 = 128 * s1 % p;              // 128 sum_t 256^t
+        const long long k1 = ((k0 - w) % p + p) % p;    // w = 2^W mod p now
+        mods[m].p = (int)p;
+        mods[m].k0 = (int)k0;
+        mods[m].k1 = (int)k1;
+        mods[m].invp = 1.0 / (double)p;
+        for (int d = 0; d < 2; ++d) {
+            const int o = 2 * m + d, ob = o / 16, row = o % 16;
+            for (int kb = 0; kb < KB; ++kb)
+                for (int g = 0; g < 4; ++g)
+                    for (int b = 0; b < 16; ++b) {
+                        const int t = 64 * kb + 16 * g + b;
+                        if (t >= 2 * L) continue;
+                        const int ln = row + 16 * g;
+                        W[(((size_t)ob * KB + kb) * 64 + ln) * 16 + b] = d ? whi[t] : wlo[t];
+                    }
+        }
+    }
+    // M and M/p_m
+    std::vector<uint32_t> M(1, 1);
+    for (int m = 0; m < nm; ++m) {
+        uint64_t c = 0;
+        for (auto &x : M) {
+            const uint64_t v = (uint64_t)x * (uint64_t)r->primes[m] + c;
+            x = (uint32_t)v;
+            c = v >> 32;
+        }
+        if (c) M.push_back((uint32_t)c);
+    }
+    std::vector<int8_t> mbh(Jpad);
+    balanced_bytes(M, Jpad, mbh.data());
+    std::vector<int8_t> T((size_t)(Jpad / 16) * KBc * 1024, 0);
+    std::vector<int8_t> dm(Jpad);
+    std::vector<uint32_t> Mm(M.size());
+    for (int m = 0; m < nm; ++m) {
+        const uint64_t p = (uint64_t)r->primes[m];
+        uint64_t rem = 0;
+        for (size_t w = M.size(); w-- > 0;) {
+            const uint64_t cur = (rem << 32) | M[w];
+            Mm[w] = (uint32_t)(cur / p);
+            rem = cur % p;
+        }
+        // (M/p_m) mod p_m = prod_{j != m} p_j mod p_m
+        long long pr = 1;
+        for (int j = 0; j < nm; ++j)
+            if (j != m) pr = pr * (r->primes[j] % (long long)p) % (long long)p;
+        mods[m].cinv = (int)modinv(pr, (long long)p);
+        balanced_bytes(Mm, Jpad, dm.data());
+        for (int d = 0; d < 2; ++d) {
+            const int k = 2 * m + d, kb = k / 64, g = (k % 64) / 16, b = k % 16;
+            for (int j = 0; j < Jpad; ++j) {
+                const int8_t v = d == 0 ? dm[j] : (j ? dm[j - 1] : (int8_t)0);
+                const int jb = j / 16, ln = (j % 16) + 16 * g;
+                T[(((size_t)jb * KBc + kb) * 64 + ln) * 16 + b] = v;
+            }
+        }
+    }
+    int rc = rns_alloc(r, (void **)&r->dMod, mods.size() * sizeof(RnsMod));
+    if (!rc) rc = rns_alloc(r, (void **)&r->dW, W.size());
+    if (!rc) rc = rns_alloc(r, (void **)&r->dT, T.size());
+    if (!rc) rc = rns_alloc(r, (void **)&r->dMb, mbh.size());
+    if (rc) return rc;
+    MFH_HIP(hipMemcpy(r->dMod, mods.data(), mods.size() * sizeof(RnsMod), hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(r->dW, W.data(), W.size(), hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(r->dT, T.data(), T.size(), hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(r->dMb, mbh.data(), mbh.size(), hipMemcpyHostToDevice));
+    return MFH_OK;
+}
+
+template <int KB, int EB>
+void launch_residue(const mfh_rns *r, const uint16_t *X, int sgn, uint16_t *R)
+{
+    // a workgroup covers 4 waves x 16 EB consecutive elements of one row
+    dim3 grid((r->np + 64 * EB - 1) / (64 * EB), r->np);
+    hipLaunchKernelGGL((k_rns_residue<KB, EB>), grid, dim3(256), 0, r->stream, X, r->n, r->np,
+                       r->L, sgn, (const v4i *)r->dW, (const RnsMod *)r->dMod, r->nm, R);
+}
+
+int run_residue(const mfh_rns *r, const uint16_t *X, int sgn, uint16_t *R)
+{
+    switch (r->KB) {
+    case 1: launch_residue<1, 4>(r, X, sgn, R); break;
+    case 2: launch_residue<2, 4>(r, X, sgn, R); break;
+    case 4: launch_residue<4, 4>(r, X, sgn, R); break;
+    case 8: launch_residue<8, 4>(r, X, sgn, R); break;
+    case 16: launch_residue<16, 2>(r, X, sgn, R); break;
+    default: return MFH_E_BOUND;
+    }
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+template <int EB>
+int launch_crt(const mfh_rns *r, uint16_t *out, int RL, int RLc)
+{
+    const int KBc = r->nmk / 32;
+    const size_t lds = crt_lds_bytes(EB, KBc, r->Jpad);
+    static bool attr_set = false;
+    if (!attr_set) {
+        MFH_HIP(hipFuncSetAttribute((const void *)k_rns_crt<EB>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        attr_set = true;
+    }
+    dim3 grid((r->n + 16 * EB - 1) / (16 * EB), r->n);
+    hipLaunchKernelGGL((k_rns_crt<EB>), grid, dim3(256), lds, r->stream, r->dY, r->n, r->np,
+                       r->nm, KBc, r->Jpad, (const v4i *)r->dT, r->dMb, (const RnsMod *)r->dMod,
+                       out, RL, RLc);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+void rns_mark(mfh_rns *r, int k)
+{
+    if (r->timing) (void)hipEventRecord(r->ev[k], r->stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mfh_rns_primes(int n, int L, int *primes, int cap)
+{
+    if (n < 1 || L < 1) return MFH_E_ARG;
+    std::vector<int> ps;
+    const int rc = plan_primes(n, L, ps);
+    if (rc) return rc;
+    for (int k = 0; k < (int)ps.size() && k < cap && primes; ++k) primes[k] = ps[k];
+    return (int)ps.size();
+}
+
+int mfh_rns_create(mfh_rns **out, int n, int L)
+{
+    if (!out) return MFH_E_ARG;
+    *out = nullptr;
+    // residue sums |2L 2^14| and the CRT columns |2 nmk 2^14| fit int32 far
+    // beyond these limits; the pointwise classes need 2 n 2^14 < 2^31; the
+    // CRT kernel holds 16 elements' int64 byte groups (2L+1 limbs) in LDS,
+    // which caps L at 512
+    if (n < 1 || n > 32768 || L < 1 || L > 512) return MFH_E_BOUND;
+    int cnt = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceCount(&cnt) != hipSuccess || cnt < 1) return MFH_E_NODEV;
+    if (hipGetDeviceProperties(&prop, 0) != hipSuccess ||
+        strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return MFH_E_NODEV;
+    mfh_rns *r = new mfh_rns();
+    r->n = n;
+    r->L = L;
+    r->np = (n + 127) / 128 * 128;
+    int rc = plan_primes(n, L, r->primes);
+    if (rc) { delete r; return rc; }
+    r->nm = (int)r->primes.size();
+    r->nmk = (r->nm + 31) / 32 * 32;
+    r->KB = kres_blocks(L);
+    r->Jpad = (2 * (2 * L + 1) + 63) / 64 * 64;
+    r->crt_eb = 0;
+    for (int eb : {4, 2, 1})
+        if (crt_lds_bytes(eb, r->nmk / 32, r->Jpad) <= 150 * 1024) { r->crt_eb = eb; break; }
+    if (!r->crt_eb) { delete r; return MFH_E_BOUND; }
+    r->dev = 0;
+    if (hipSetDevice(0) != hipSuccess || hipStreamCreate(&r->stream) != hipSuccess) {
+        delete r;
+        return MFH_E_HIP;
+    }
+    for (auto &e : r->ev) (void)hipEventCreate(&e);
+    const size_t res = (size_t)r->nm * r->np * r->np * 2;
+    rc = rns_tables(r);
+    if (!rc) rc = rns_alloc(r, (void **)&r->dRA, res);
+    if (!rc) rc = rns_alloc(r, (void **)&r->dRB, res);
+    if (!rc) rc = rns_alloc(r, (void **)&r->dY, res);
+    if (!rc) rc = rns_alloc(r, (void **)&r->dBt, (size_t)L * n * n * 2);
+    if (rc) { mfh_rns_destroy(r); return rc; }
+    *out = r;
+    return MFH_OK;
+}
+
+void mfh_rns_destroy(mfh_rns *r)
+{
+    if (!r) return;
+    if (r->stream) (void)hipStreamSynchronize(r->stream);
+    void *bufs[] = {r->dMod, r->dW, r->dT, r->dMb, r->dRA, r->dRB, r->dY, r->dBt};
+    for (void *b : bufs)
+        if (b) (void)hipFree(b);
+    for (auto &e : r->ev)
+        if (e) (void)hipEventDestroy(e);
+    if (r->stream) (void)hipStreamDestroy(r->stream);
+    delete r;
+}
+
+int mfh_rns_info(const mfh_rns *r, int *nmod, int *np_, size_t *bytes)
+{
+    if (!r) return MFH_E_ARG;
+    if (nmod) *nmod = r->nm;
+    if (np_) *np_ = r->np;
+    if (bytes) *bytes = r->bytes;
+    return MFH_OK;
+}
+
+int mfh_rns_residues_dev(mfh_rns *r, int in_kind, const void *dX, void *dR)
+{
+    if (!r || !dX || !dR) return MFH_E_ARG;
+    if (in_kind != MFH_IN_U16 && in_kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
+    return run_residue(r, (const uint16_t *)dX, in_kind == MFH_IN_U16_SIGNED, (uint16_t *)dR);
+}
+
+int mfh_rns_mm_dev(mfh_rns *r, int in_kind, const void *dA, const void *dB, void *dOut, int RL)
+{
+    if (!r || !dA || !dB || !dOut || RL < 1) return MFH_E_ARG;
+    if (in_kind != MFH_IN_U16 && in_kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
+    const int sgn = in_kind == MFH_IN_U16_SIGNED;
+    rns_mark(r, 0);
+    int rc = mfh_launch_transpose(dB, r->dBt, r->L, r->n, 2, r->stream);
+    if (!rc) rc = run_residue(r, (const uint16_t *)dA, sgn, r->dRA);
+    if (!rc) rc = run_residue(r, r->dBt, sgn, r->dRB);
+    if (rc) return rc;
+    rns_mark(r, 1);
+    const int T = (r->np / 128) * (r->np / 128);
+    hipLaunchKernelGGL(k_rns_pointwise, dim3(r->nm * T), dim3(256), 0, r->stream,
+                       (const uint16_t *)r->dRA, (const uint16_t *)r->dRB,
+                       (const RnsMod *)r->dMod, r->nm, r->np, r->dY);
+    MFH_HIP(hipGetLastError());
+    rns_mark(r, 2);
+    const int RLc = std::min(RL, 2 * r->L + 1);
+    switch (r->crt_eb) {
+    case 4: rc = launch_crt<4>(r, (uint16_t *)dOut, RL, RLc); break;
+    case 2: rc = launch_crt<2>(r, (uint16_t *)dOut, RL, RLc); break;
+    default: rc = launch_crt<1>(r, (uint16_t *)dOut, RL, RLc); break;
+    }
+    if (rc) return rc;
+    rns_mark(r, 3);
+    return MFH_OK;
+}
+
+int mfh_rns_mm(mfh_rns *r, int in_kind, const uint16_t *A, const uint16_t *B, uint16_t *out,
+               int RL)
+{
+    if (!r || !A || !B || !out || RL < 1) return MFH_E_ARG;
+    const size_t in = (size_t)r->L * r->n * r->n * 2, ob = (size_t)RL * r->n * r->n * 2;
+    void *dA = nullptr, *dB = nullptr, *dO = nullptr;
+    int rc = MFH_OK;
+    if (hipMalloc(&dA, in) != hipSuccess || hipMalloc(&dB, in) != hipSuccess ||
+        hipMalloc(&dO, ob) != hipSuccess)
+        rc = MFH_E_NOMEM;
+    if (!rc && (hipMemcpyAsync(dA, A, in, hipMemcpyHostToDevice, r->stream) != hipSuccess ||
+                hipMemcpyAsync(dB, B, in, hipMemcpyHostToDevice, r->stream) != hipSuccess))
+        rc = MFH_E_HIP;
+    if (!rc) rc = mfh_rns_mm_dev(r, in_kind, dA, dB, dO, RL);
+    if (!rc && hipMemcpyAsync(out, dO, ob, hipMemcpyDeviceToHost, r->stream) != hipSuccess)
+        rc = MFH_E_HIP;
+    if (hipStreamSynchronize(r->stream) != hipSuccess && !rc) rc = MFH_E_HIP;
+    for (void *p : {dA, dB, dO})
+        if (p) (void)hipFree(p);
+    return rc;
+}
+
+int mfh_rns_sync(mfh_rns *r)
+{
+    if (!r) return MFH_E_ARG;
+    MFH_HIP(hipStreamSynchronize(r->stream));
+    return MFH_OK;
+}
+
+int mfh_rns_set_timing(mfh_rns *r, int enable)
+{
+    if (!r) return MFH_E_ARG;
+    r->timing = enable ? 1 : 0;
+    return MFH_OK;
+}
+
+int mfh_rns_stage_times(const mfh_rns *r, float ms[4])
+{
+    if (!r || !ms) return MFH_E_ARG;
+    MFH_HIP(hipEventSynchronize(r->ev[3]));
+    for (int k = 0; k < 3; ++k) MFH_HIP(hipEventElapsedTime(&ms[k], r->ev[k], r->ev[k + 1]));
+    MFH_HIP(hipEventElapsedTime(&ms[3], r->ev[0], r->ev[3]));
+    return MFH_OK;
+}
+
+int mfh_rns_work(const mfh_rns *r, double *res_ops, double *pw_ops, double *crt_ops)
+{
+    if (!r) return MFH_E_ARG;
+    const double np3 = (double)r->np * r->np * r->np, np2 = (double)r->np * r->np;
+    if (res_ops) *res_ops = 2.0 * 2 * np2 * (64.0 * r->KB) * (2.0 * r->nm);
+    if (pw_ops) *pw_ops = (double)r->nm * 4 * 2 * np3;
+    if (crt_ops) *crt_ops = 2.0 * r->n * r->n * (2.0 * r->nmk) * r->Jpad;
+    return MFH_OK;
+}
+
+}  // extern "C"

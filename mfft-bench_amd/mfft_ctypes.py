@@ -140,6 +140,16 @@ def load(path=None):
         "mfft_last_error": ([], i), "mfft_strerror": ([i], C.c_char_p),
         "kernel_name": ([i], C.c_char_p), "kernel_from_name": ([C.c_char_p], i),
         "now_sec": ([], C.c_double),
+        "mfh_rns_primes": ([i, i, vp, i], i),
+        "mfh_rns_create": ([C.POINTER(vp), i, i], i), "mfh_rns_destroy": ([vp], None),
+        "mfh_rns_info": ([vp, C.POINTER(i), C.POINTER(i), C.POINTER(sz)], i),
+        "mfh_rns_mm_dev": ([vp, i, vp, vp, vp, i], i),
+        "mfh_rns_mm": ([vp, i, vp, vp, vp, i], i),
+        "mfh_rns_residues_dev": ([vp, i, vp, vp], i),
+        "mfh_rns_sync": ([vp], i), "mfh_rns_set_timing": ([vp, i], i),
+        "mfh_rns_stage_times": ([vp, C.POINTER(C.c_float)], i),
+        "mfh_rns_work": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                          C.POINTER(C.c_double)], i),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -268,6 +278,90 @@ class Ctx:
         check(self.lib.mfh_conv_stages(self.h, _p(A32), _p(B32), stage, _p(out), out.size,
                                        info), "mfh_conv_stages")
         return tuple(int(v) for v in info), out
+
+
+def rns_primes(n, L):
+    """the primes of the multi-modular product of n x n matrices of L limbs
+    (host planning, no device needed)"""
+    lib = load()
+    cnt = lib.mfh_rns_primes(n, L, None, 0)
+    check(min(cnt, 0), "mfh_rns_primes")
+    out = np.zeros(cnt, dtype=np.int32)
+    lib.mfh_rns_primes(n, L, _p(out), cnt)
+    return out
+
+
+class Rns:
+    """One multi-modular product context (mfh_rns_*): tables and workspace for
+    n x n matrices of L limbs."""
+
+    def __init__(self, n, L):
+        self.lib = load()
+        self.n, self.L = n, L
+        h = C.c_void_p()
+        check(self.lib.mfh_rns_create(C.byref(h), n, L), "mfh_rns_create")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.mfh_rns_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self):
+        """(primes, padded n, device bytes)"""
+        nm, np_, b = C.c_int(), C.c_int(), C.c_size_t()
+        check(self.lib.mfh_rns_info(self.h, C.byref(nm), C.byref(np_), C.byref(b)))
+        return nm.value, np_.value, b.value
+
+    def mm(self, A, B, RL=None, signed=False):
+        RL = RL or 2 * self.L + 1
+        out = np.empty(RL * self.n * self.n, dtype=np.uint16)
+        kind = MFH_IN_U16_SIGNED if signed else MFH_IN_U16
+        check(self.lib.mfh_rns_mm(self.h, kind, _p(A), _p(B), _p(out), RL), "mfh_rns_mm")
+        return out
+
+    def mm_dev(self, dA, dB, dOut, RL, signed=False):
+        kind = MFH_IN_U16_SIGNED if signed else MFH_IN_U16
+        check(self.lib.mfh_rns_mm_dev(self.h, kind, dA, dB, dOut, RL), "mfh_rns_mm_dev")
+
+    def residues(self, X, signed=False):
+        """digit-pair residues [primes][np][np] of one operand (rows r, inner k)"""
+        nm, np_, _ = self.info()
+        dX = DevBuf(max(X.nbytes, 16))
+        dX.upload(X)
+        dR = DevBuf(nm * np_ * np_ * 2)
+        kind = MFH_IN_U16_SIGNED if signed else MFH_IN_U16
+        check(self.lib.mfh_rns_residues_dev(self.h, kind, dX.ptr, dR.ptr), "mfh_rns_residues_dev")
+        self.sync()
+        return dR.download(np.uint16, nm * np_ * np_).reshape(nm, np_, np_)
+
+    def sync(self):
+        check(self.lib.mfh_rns_sync(self.h), "mfh_rns_sync")
+
+    def set_timing(self, on=True):
+        check(self.lib.mfh_rns_set_timing(self.h, int(on)))
+
+    def stage_times(self):
+        ms = (C.c_float * 4)()
+        check(self.lib.mfh_rns_stage_times(self.h, ms), "mfh_rns_stage_times")
+        return list(ms)
+
+    def work(self):
+        a, b, c = C.c_double(), C.c_double(), C.c_double()
+        check(self.lib.mfh_rns_work(self.h, C.byref(a), C.byref(b), C.byref(c)))
+        return a.value, b.value, c.value
 
 
 class DevBuf:
