@@ -189,6 +189,56 @@ def cpu_baseline(n, L, nprod_total):
                         f"mm_mfft at n={ns} ({rest_small:.3f} s) x {scale:.0f}; extrapolated"))
 
 
+def rns_measure(n, L, kind, dA, dB, steps, warmup, want=None):
+    """The multi-modular product (mfh_rns_*) of the same device-resident
+    inputs: ms per product, stage times, the int8 GEMMs it issues, and
+    whether its limbs equal `want` (the MFFT product's)."""
+    import numpy as np
+    import mfft_ctypes as M
+    RL = 2 * L + 1
+    lib = M.load()
+    try:
+        r = M.Rns(n, L)
+    except M.MfftError as e:
+        log(f"[bench] multi-modular n={n} L={L}: {e}")
+        return None
+    dO = M.DevBuf(RL * n * n * 2)
+    step = lambda: M.check(lib.mfh_rns_mm_dev(r.h, kind, dA.ptr, dB.ptr, dO.ptr, RL),
+                           "mfh_rns_mm_dev")
+    for _ in range(max(1, warmup)):
+        step()
+    r.sync()
+    r.set_timing(True)
+    stage = np.zeros(4)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+        stage += np.array(r.stage_times())
+    r.sync()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    r.set_timing(False)
+    st = stage / steps
+    nm, np_, nbytes = r.info()
+    res_ops, pw_ops, crt_ops = r.work()
+    equal = None
+    if want is not None:
+        equal = bool(np.array_equal(dO.download(np.uint16, RL * n * n), want))
+    dO.free()
+    r.close()
+    log(f"[bench] multi-modular: {ms:.3f} ms/product, stages(ms) residues {st[0]:.3f} "
+        f"per-prime GEMMs {st[1]:.3f} CRT+carry {st[2]:.3f}; {nm} primes; equal to MFFT: {equal}")
+    return {"ms_per_step": round(ms, 3), "primes": nm,
+            "int8_gemms_per_product": 4 * nm,
+            "stage_ms": {"residues": round(st[0], 3), "per_prime_gemms": round(st[1], 3),
+                         "crt_carry": round(st[2], 3)},
+            "int8_ops": {"residues": res_ops, "per_prime_gemms": pw_ops, "crt": crt_ops},
+            "per_prime_gemm_tops": round(pw_ops / (st[1] * 1e-3) / 1e12, 1),
+            "device_bytes": nbytes, "equal_to_mfft": equal,
+            "note": ("exact product by residues mod 16-bit primes (mfh_rns_mm_dev), same "
+                     "inputs and output limbs as the MFFT product; no counterpart in the "
+                     "reference")}
+
+
 def method_table(args):
     """The reference bench's result table (src/main.c:137-165) for the device
     methods on one exact-track workload: the schoolbook (limbplane, the
@@ -277,6 +327,18 @@ def method_table_for(n, W, ekind, args, header=True):
         ring, _ = ctx.pointwise_info()
         rows.append([name, "hip", p.nprod, p.NB * ring, 0, secs, out])
         ctx.close()
+    # the multi-modular product (no reference counterpart): `products` and
+    # `issued` count its per-prime n x n products (4 int8 GEMMs each)
+    try:
+        rns = M.Rns(n, L)
+        secs = timed(lambda: M.check(lib.mfh_rns_mm_dev(rns.h, kind, dA.ptr, dB.ptr, dO.ptr, RL)),
+                     max(1, args.steps))
+        rns.sync()
+        nm = rns.info()[0]
+        rows.append(["rns", "hip", nm, nm, 0, secs, dO.download(np.uint16, RL * n * n)])
+        rns.close()
+    except M.MfftError as e:
+        log(f"[table] rns n={n} W={W}: {e}")
     A = host_rand_u16(n, L, 12345)
     B = host_rand_u16(n, L, 12345 ^ 0xABCDEF)
     base = rows[0][5]
@@ -318,6 +380,8 @@ def main():
                     help="with --n/--bits: two's complement entries")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-verify", action="store_true")
+    ap.add_argument("--no-rns", action="store_true",
+                    help="skip the multi-modular product reported beside the MFFT one")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run the plain copy kernel over MIB MiB, --steps times (the "
                          "known-size kernel that HBM byte counters are calibrated against)")
@@ -466,6 +530,11 @@ def main():
     except (OSError, ValueError):
         pass
 
+    mm = None
+    if not fp32 and not args.no_rns:
+        mfft_out = dO.download(np.uint16, RL * n * n)
+        mm = rns_measure(n, L, kind, dA, dB, args.steps, args.warmup, mfft_out)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the reference CPU path on a bounded sample ...")
@@ -514,6 +583,7 @@ def main():
                      "note": "int8 tera-operations per second issued by the pointwise kernel "
                              "(dense int8 MFMA peak 5.0 POP/s)"},
         "cpu_baseline": cpu,
+        "multimodular": mm,
     }
     print(json.dumps(line), flush=True)
     for b in (dA, dB, dO):

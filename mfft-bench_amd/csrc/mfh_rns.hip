@@ -128,23 +128,42 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
             uint32_t d[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                // unconditional loads (limb index clamped, the value selected
+                // after): conditional ones each became a branch with a wait
                 const int u = 32 * kb + 8 * grp + 2 * q;
-                const uint32_t x0 = (ok[cb] && u < L) ? base[(size_t)u * nn] : 0;
-                const uint32_t x1 = (ok[cb] && u + 1 < L) ? base[(size_t)(u + 1) * nn] : 0;
+                const uint32_t v0 = base[(size_t)min(u, L - 1) * nn];
+                const uint32_t v1 = base[(size_t)min(u + 1, L - 1) * nn];
+                const uint32_t x0 = (ok[cb] && u < L) ? v0 : 0;
+                const uint32_t x1 = (ok[cb] && u + 1 < L) ? v1 : 0;
                 d[q] = (x0 | (x1 << 16)) ^ 0x80808080u;      // bytes b - 128
             }
             ef[kb][cb] = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
         }
-        sb[cb] = (sgn && ok[cb]) ? (base[(size_t)(L - 1) * nn] >> 15) : 0;
+        const int top = base[(size_t)(L - 1) * nn] >> 15;
+        sb[cb] = (sgn && ok[cb]) ? top : 0;
     }
+    // the weight fragments of output block ob + 1 are loaded while block ob
+    // is multiplied (up to 8 k blocks; beyond that the registers hold the
+    // element fragments)
+    constexpr int PF = KB <= 8 ? KB : 0;
+    v4i wn[PF > 0 ? PF : 1];
+#pragma unroll
+    for (int kb = 0; kb < PF; ++kb) wn[kb] = W[(size_t)kb * 64 + lane];
 #pragma unroll 1
     for (int ob = 0; ob < nm / 8; ++ob) {
         v4i acc[EB];
 #pragma unroll
         for (int cb = 0; cb < EB; ++cb) acc[cb] = v4i{0, 0, 0, 0};
+        v4i wc[PF > 0 ? PF : 1];
+#pragma unroll
+        for (int kb = 0; kb < PF; ++kb) wc[kb] = wn[kb];
+        if (PF && ob + 1 < nm / 8) {
+#pragma unroll
+            for (int kb = 0; kb < PF; ++kb) wn[kb] = W[((size_t)(ob + 1) * KB + kb) * 64 + lane];
+        }
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-            const v4i w = W[((size_t)ob * KB + kb) * 64 + lane];
+            const v4i w = PF ? wc[kb < PF ? kb : 0] : W[((size_t)ob * KB + kb) * 64 + lane];
 #pragma unroll
             for (int cb = 0; cb < EB; ++cb)
                 acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, ef[kb][cb], acc[cb], 0, 0, 0);
@@ -277,18 +296,23 @@ __global__ __launch_bounds__(256) void k_rns_pointwise(const uint16_t *__restric
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc.hh[a][b] = acc.md[a][b] = acc.ll[a][b] = v4i{0, 0, 0, 0};
     const int nkb = np_ / 64;
+    // Every step issues exactly 8 copies per wave (past the last block it
+    // copies the last block again, into the stage just retired), so the
+    // outstanding copies are the same on every path: the compiler's own
+    // waits then stay at vmcnt(8) (with a conditional issue it waited for
+    // all copies, the ones just issued included, before every block).
     rns_issue(s0, a0, b0, rowb, 0, wave, off);
-    if (nkb > 1) rns_issue(s1, a0, b0, rowb, 1, wave, off);
+    rns_issue(s1, a0, b0, rowb, min(1, nkb - 1), wave, off);
     // Stage kb % 3 is complete once this wave's copies of kb are (only those
     // of kb + 1 may remain: 8 per wave) and every wave has passed the
     // barrier; the barrier also retires every read of stage (kb + 2) % 3
     // (block kb - 1), which the copies of kb + 2 then overwrite.
-#define RNS_STEP(S, SN, KB)                                                   \
-    {                                                                         \
-        if ((KB) + 1 < nkb) wait_vm_lgkm<8>(); else wait_vm_lgkm<0>();        \
-        __builtin_amdgcn_s_barrier();                                         \
-        if ((KB) + 2 < nkb) rns_issue(SN, a0, b0, rowb, (KB) + 2, wave, off); \
-        rns_compute(S, wi, wj, lane, acc);                                    \
+#define RNS_STEP(S, SN, KB)                                                    \
+    {                                                                          \
+        wait_vm_lgkm<8>();                                                     \
+        __builtin_amdgcn_s_barrier();                                          \
+        rns_issue(SN, a0, b0, rowb, min((KB) + 2, nkb - 1), wave, off);        \
+        rns_compute(S, wi, wj, lane, acc);                                     \
     }
     // no exits inside the unrolled body: with them the accumulators were
     // copied at every exit and spilled
@@ -323,90 +347,129 @@ __global__ __launch_bounds__(256) void k_rns_pointwise(const uint16_t *__restric
 
 // ---- 3. CRT and carry ------------------------------------------------------
 // E = 16 EB elements (row i = blockIdx.y, columns j0 .. j0+E-1) per
-// workgroup.  LDS: the y digit pairs of the E elements as MFMA B fragments
-// [KBc][EB][64 lanes][16 B] (fragment (kb, cb): element 16 cb + l%16, the
-// digit pairs of primes 32 kb + 8 (l/16) .. +7), the int64 groups
-// [G = Jpad/4][E], and the carry lookahead's run data.  T holds the A
-// fragments [Jpad/16][KBc][64][16 B]: row j (output byte) of k = 2m + d is
-// byte j of M/p_m (d = 0) or of 256 M/p_m (d = 1), zero for m >= nm.
+// workgroup of 8 waves.  LDS: the y digit pairs of the E elements as MFMA B
+// fragments [KBc][EB][64 lanes][16 B] (fragment (kb, cb): element
+// 16 cb + l%16, the digit pairs of primes 32 kb + 8 (l/16) .. +7), the
+// int64 groups [G = Jpad/4][E], q's fp64 sums, and the carry lookahead's run
+// data.  T holds the A fragments [Jpad/16][KBc][64][16 B]: row j (output
+// byte) of k = 2m + d is byte j of M/p_m (d = 0) or of 256 M/p_m (d = 1),
+// zero for m >= nm.
+constexpr int kCrtThreads = 512;
+constexpr int kCrtBatch = 4;       // k blocks of T fragments loaded at once
+
 template <int EB>
-__global__ __launch_bounds__(256) void k_rns_crt(const uint16_t *__restrict__ Y, int n, int np_,
-                                                 int nm, int KBc, int Jpad,
-                                                 const v4i *__restrict__ T,
-                                                 const int8_t *__restrict__ mb,
-                                                 const RnsMod *__restrict__ mods,
-                                                 uint16_t *__restrict__ out, int RL, int RLc)
+__global__ __launch_bounds__(kCrtThreads) void k_rns_crt(
+    const uint16_t *__restrict__ Y, int n, int np_, int nm, int KBc, int Jpad,
+    const v4i *__restrict__ T, const int8_t *__restrict__ mb, const RnsMod *__restrict__ mods,
+    uint16_t *__restrict__ out, int RL, int RLc)
 {
-    constexpr int E = 16 * EB, SEGS = 256 / E;
+    constexpr int NT = kCrtThreads, E = 16 * EB, SEGS = NT / E, NW = NT / 64;
+    constexpr int EG = E / 8, MS = NT / EG;    // groups of 8 elements, prime slots
     extern __shared__ __align__(16) unsigned char smem[];
     v4i *yl = (v4i *)smem;                                        // KBc*EB*64
     long long *grp = (long long *)(yl + (size_t)KBc * EB * 64);  // [G][E]
     const int G = Jpad / 4;
-    double *qs = (double *)(grp + (size_t)G * E);                 // [256]
-    long long *segc = (long long *)(qs + 256);                    // [SEGS][E] x 4
-    long long *seglo = segc + 256, *seghi = seglo + 256, *segin = seghi + 256;
-    int *qv = (int *)(segin + 256);                               // [E]
+    long long *segc = grp + (size_t)G * E;                        // [SEGS][E] x 4
+    long long *seglo = segc + NT, *seghi = seglo + NT, *segin = seghi + NT;
+    double *qs = (double *)(segin + NT);                          // [E]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i = blockIdx.y, j0 = blockIdx.x * E;
     const size_t npp = (size_t)np_ * np_, nn = (size_t)n * n;
+    if (tid < E) qs[tid] = 0;
+    __syncthreads();
 
-    // 1. y digit pairs into LDS, and the partial sums of y_m / p_m
+    // 1. y digit pairs into LDS (16-byte loads of 8 elements of one prime,
+    //    a batch of them in flight per thread), and sum_m y_m / p_m.  Columns
+    //    j0+E <= np; those at or beyond n hold y = 0 (their operand rows
+    //    were zero), so no element needs a check here.
     {
-        const int e = tid % E, mg = tid / E;
-        const bool ev = j0 + e < n;
-        const uint16_t *src = Y + (size_t)i * np_ + j0 + e;
+        const int eg = tid % EG, ms = tid / EG;
+        const uint16_t *src = Y + (size_t)i * np_ + j0 + 8 * eg;
         uint16_t *yw = (uint16_t *)yl;
-        double qsum = 0;
-        for (int m = mg; m < 32 * KBc; m += SEGS) {
-            uint16_t w = 0;
-            if (m < nm && ev) {
-                w = src[(size_t)m * npp];
-                qsum += (double)rns_unpair(w) * mods[m].invp;
+        double qp[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) qp[q] = 0;
+        constexpr int BATCH = 8;
+        for (int m0 = ms; m0 < 32 * KBc; m0 += MS * BATCH) {
+            uint4 w[BATCH];
+            double ip[BATCH];
+#pragma unroll
+            for (int b = 0; b < BATCH; ++b) {
+                const int m = m0 + b * MS;
+                if (m < nm) {
+                    w[b] = *(const uint4 *)(src + (size_t)m * npp);
+                    ip[b] = mods[m].invp;
+                } else {
+                    w[b] = uint4{0, 0, 0, 0};
+                    ip[b] = 0;
+                }
             }
-            const int kb = m >> 5, mq = m & 31;
-            const int ln = (e & 15) + 16 * (mq >> 3);
-            yw[(((size_t)kb * EB + (e >> 4)) * 64 + ln) * 8 + (mq & 7)] = w;
+#pragma unroll
+            for (int b = 0; b < BATCH; ++b) {
+                const int m = m0 + b * MS;
+                if (m < 32 * KBc) {
+                    const int kb = m >> 5, mq = m & 31;
+                    const uint32_t ww[4] = {w[b].x, w[b].y, w[b].z, w[b].w};
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {
+                        const uint16_t v = (uint16_t)(ww[q >> 1] >> (16 * (q & 1)));
+                        const int e = 8 * eg + q;
+                        const int ln = (e & 15) + 16 * (mq >> 3);
+                        yw[(((size_t)kb * EB + (e >> 4)) * 64 + ln) * 8 + (mq & 7)] = v;
+                        qp[q] += (double)rns_unpair(v) * ip[b];
+                    }
+                }
+            }
         }
-        qs[tid] = qsum;
-    }
-    __syncthreads();
-    if (tid < E) {
-        double s = 0;
-        for (int r = 0; r < SEGS; ++r) s += qs[r * E + tid];
-        qv[tid] = (int)rint(s);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) atomicAdd(&qs[8 * eg + q], qp[q]);
     }
     __syncthreads();
 
-    // 2. byte columns: GEMM over the y digits, q M subtracted, groups of 4
+    // 2. byte columns: GEMM over the y digits, q M subtracted, groups of 4.
+    //    A wave takes chunks of 64 output bytes (4 fragment rows); the T
+    //    fragments of a chunk stream in batches of kCrtBatch k blocks, the
+    //    next batch loaded while the current one is multiplied.
     const int nch = Jpad / 64;
-    for (int ch = wave; ch < nch; ch += 4) {
+    for (int ch = wave; ch < nch; ch += NW) {
         v4i acc[4][EB];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
             for (int cb = 0; cb < EB; ++cb) acc[jj][cb] = v4i{0, 0, 0, 0};
         const v4i *tp = T + (size_t)4 * ch * KBc * 64 + lane;
-        v4i tf[4], tn[4];
+        v4i ta[kCrtBatch][4], tb[kCrtBatch][4];
+        auto load = [&](v4i (&t)[kCrtBatch][4], int kb0) {
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) tf[jj] = tp[(size_t)jj * KBc * 64];
-#pragma unroll 1
-        for (int kb = 0; kb < KBc; ++kb) {
-            if (kb + 1 < KBc) {
+            for (int b = 0; b < kCrtBatch; ++b)
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) tn[jj] = tp[((size_t)jj * KBc + kb + 1) * 64];
-            }
-            v4i yf[EB];
+                for (int jj = 0; jj < 4; ++jj)
+                    t[b][jj] = kb0 + b < KBc ? tp[((size_t)jj * KBc + kb0 + b) * 64]
+                                             : v4i{0, 0, 0, 0};
+        };
+        auto mul = [&](const v4i (&t)[kCrtBatch][4], int kb0) {
 #pragma unroll
-            for (int cb = 0; cb < EB; ++cb) yf[cb] = yl[((size_t)kb * EB + cb) * 64 + lane];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
+            for (int b = 0; b < kCrtBatch; ++b) {
+                if (kb0 + b >= KBc) continue;
+                v4i yf[EB];
 #pragma unroll
                 for (int cb = 0; cb < EB; ++cb)
-                    acc[jj][cb] =
-                        __builtin_amdgcn_mfma_i32_16x16x64_i8(tf[jj], yf[cb], acc[jj][cb], 0, 0, 0);
+                    yf[cb] = yl[((size_t)(kb0 + b) * EB + cb) * 64 + lane];
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) tf[jj] = tn[jj];
+                for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                    for (int cb = 0; cb < EB; ++cb)
+                        acc[jj][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(t[b][jj], yf[cb],
+                                                                             acc[jj][cb], 0, 0, 0);
+            }
+        };
+        load(ta, 0);
+        for (int kb0 = 0; kb0 < KBc; kb0 += 2 * kCrtBatch) {
+            load(tb, kb0 + kCrtBatch);
+            mul(ta, kb0);
+            load(ta, kb0 + 2 * kCrtBatch);
+            mul(tb, kb0 + kCrtBatch);
         }
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj)
@@ -414,7 +477,7 @@ __global__ __launch_bounds__(256) void k_rns_crt(const uint16_t *__restrict__ Y,
             for (int cb = 0; cb < EB; ++cb) {
                 const int el = 16 * cb + (lane & 15);
                 const int gi = 4 * (4 * ch + jj) + (lane >> 4);
-                const long long q = qv[el];
+                const long long q = (long long)rint(qs[el]);
                 long long g = 0;
 #pragma unroll
                 for (int v = 3; v >= 0; --v)
@@ -494,7 +557,7 @@ __global__ __launch_bounds__(256) void k_rns_crt(const uint16_t *__restrict__ Y,
 size_t crt_lds_bytes(int EB, int KBc, int Jpad)
 {
     const int E = 16 * EB;
-    return (size_t)KBc * EB * 1024 + (size_t)(Jpad / 4) * E * 8 + 256 * 8 + 4 * 256 * 8 + E * 4;
+    return (size_t)KBc * EB * 1024 + (size_t)(Jpad / 4) * E * 8 + 4 * kCrtThreads * 8 + E * 8;
 }
 
 // ---- host planning ---------------------------------------------------------
@@ -717,7 +780,7 @@ int launch_crt(const mfh_rns *r, uint16_t *out, int RL, int RLc)
         attr_set = true;
     }
     dim3 grid((r->n + 16 * EB - 1) / (16 * EB), r->n);
-    hipLaunchKernelGGL((k_rns_crt<EB>), grid, dim3(256), lds, r->stream, r->dY, r->n, r->np,
+    hipLaunchKernelGGL((k_rns_crt<EB>), grid, dim3(kCrtThreads), lds, r->stream, r->dY, r->n, r->np,
                        r->nm, KBc, r->Jpad, (const v4i *)r->dT, r->dMb, (const RnsMod *)r->dMod,
                        out, RL, RLc);
     MFH_HIP(hipGetLastError());
