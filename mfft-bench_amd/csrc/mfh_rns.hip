@@ -41,6 +41,7 @@
 // 16 k bytes 16 (l/16) .. +15 (A and B use the same k order); results: lane
 // l, value v is row 4 (l/16) + v, column l%16.
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -53,33 +54,35 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // per prime: p, the residue offsets k0 = 128 sum_t w_t and k1 = k0 - 2^W
-// (mod p, in [0, p)), cinv = (M/p)^-1 mod p, and 1/p
+// (mod p, in [0, p)), cinv = (M/p)^-1 mod p, 1/p, and the offsets of the
+// scaled residues (B's, times cinv): k0b = k0 cinv, k1b = k1 cinv (mod p)
 struct RnsMod {
     int p, k0, k1, cinv;
     double invp;
+    int k0b, k1b;
 };
-static_assert(sizeof(RnsMod) == 24, "RnsMod layout");
+static_assert(sizeof(RnsMod) == 32, "RnsMod layout");
 
 constexpr int kPrimeMax = 65279;   // (p-1)/2 <= 32639 keeps the hi digit in int8
 constexpr int kPrimeMin = 16411;   // smallest prime the plans draw on
 
-// balanced residue of an exact integer value held in a double (|v| < 2^53)
+// Balanced residue of an exact integer v held in a double, |v| <= 2^46:
+// q = rint(v / p) computed as rint(v * fl(1/p)), r = v - q p (exact, the
+// result is small).  v * fl(1/p) errs from v/p by at most 2^-22, while v/p
+// (p odd) is at least 1/(2p) > 2^-17 from any half-integer, so q is the
+// nearest integer and |r| <= (p-1)/2 with no correction step.
 __device__ __forceinline__ int rns_reduce(double v, int p, double invp)
 {
     const double q = rint(v * invp);
-    int r = (int)fma(-q, (double)p, v);            // exact: the result is small
-    const int h = p >> 1;
-    if (r > h) r -= p;
-    else if (r < -h) r += p;
-    return r;
+    return (int)fma(-q, (double)p, v);
 }
 
-// digit pair of a balanced residue, |r| <= 32639
+// digit pair of a balanced residue r, |r| <= 32639: with t = r + 128,
+// lo = (t & 255) - 128 and hi = t >> 8, so the pair lo | hi << 8 (as bytes)
+// is t ^ 0x80 in the low 16 bits
 __device__ __forceinline__ uint16_t rns_pair(int r)
 {
-    const int lo = ((r + 128) & 255) - 128;
-    const int hi = (r - lo) >> 8;
-    return (uint16_t)((lo & 255) | ((hi & 255) << 8));
+    return (uint16_t)((r + 128) ^ 0x80);
 }
 
 __device__ __forceinline__ int rns_unpair(uint16_t w)
@@ -102,9 +105,12 @@ __device__ __forceinline__ void wait_vm_lgkm()
 // fragments of all KB 64-byte k blocks in registers; W holds the weight
 // fragments [nm/8][KB][64 lanes][16 B]: fragment (ob, kb) row o = 16 ob + l%16
 // is digit o%2 (0: lo, 1: hi) of w_{8 ob + o/2, t}, t = 64 kb + byte.
+// scaled: W holds the weights times cinv (B's residues, so that the
+// per-prime products come out already multiplied by cinv), with the offsets
+// k0b / k1b
 template <int KB, int EB>
 __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict__ X, int n,
-                                                     int np_, int L, int sgn,
+                                                     int np_, int L, int sgn, int scaled,
                                                      const v4i *__restrict__ W,
                                                      const RnsMod *__restrict__ mods, int nm,
                                                      uint16_t *__restrict__ R)
@@ -179,8 +185,9 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
                 if (k >= np_) continue;
                 uint16_t w = 0;
                 if (ok[cb]) {
+                    const int off = scaled ? (sb[cb] ? md.k1b : md.k0b) : (sb[cb] ? md.k1 : md.k0);
                     const double v = (double)acc[cb][2 * mm + 1] * 256.0 +
-                                     (double)acc[cb][2 * mm] + (double)(sb[cb] ? md.k1 : md.k0);
+                                     (double)acc[cb][2 * mm] + (double)off;
                     w = rns_pair(rns_reduce(v, md.p, md.invp));
                 }
                 dst[k] = w;
@@ -203,12 +210,14 @@ struct PwStage {
     v4i b[8][128];
 };
 
+// NW waves issue the 32 copies of a stage (16 A, 16 B), 32 / NW each
+template <int NW>
 __device__ __forceinline__ void rns_issue(PwStage &st, const char *a0, const char *b0,
                                           size_t rowb, int kb, int wave, const uint32_t off[2])
 {
 #pragma unroll
-    for (int ii = 0; ii < 8; ++ii) {
-        const int idx = wave + 4 * ii;               // 0..31
+    for (int ii = 0; ii < 32 / NW; ++ii) {
+        const int idx = wave + NW * ii;              // 0..31
         const int opnd = idx >> 4, rb = (idx & 15) >> 1, sh = idx & 1;
         const char *src = (opnd ? b0 : a0) + (size_t)16 * rb * rowb + (size_t)kb * 128 + off[sh];
         v4i *dst = opnd ? &st.b[rb][64 * sh] : &st.a[rb][64 * sh];
@@ -229,120 +238,213 @@ __device__ __forceinline__ void rns_split(const v4i d0, const v4i d1, v4i &lo, v
              (int)__builtin_amdgcn_perm((uint32_t)d1.w, (uint32_t)d1.z, 0x07050301u)};
 }
 
+// a wave's accumulators: AB row blocks x 4 column blocks of 16 x 16, three
+// classes each
+template <int AB>
 struct PwAcc {
-    v4i hh[4][4], md[4][4], ll[4][4];
+    v4i hh[AB][4], md[AB][4], ll[AB][4];
 };
 
+template <int AB>
 __device__ __forceinline__ void rns_compute(const PwStage &st, int wi, int wj, int lane,
-                                            PwAcc &c)
+                                            PwAcc<AB> &c)
 {
     const int c0 = 32 * (lane >> 4) + (lane & 15);
-    v4i alo[4], ahi[4], blo[4], bhi[4];
+    // every fragment read of the block issued before any is used (a fence
+    // keeps the compiler from waiting for each pair before the next)
+    v4i ra[AB][2], rb[4][2];
 #pragma unroll
-    for (int a = 0; a < 4; ++a) rns_split(st.a[4 * wi + a][c0], st.a[4 * wi + a][c0 + 16], alo[a], ahi[a]);
+    for (int a = 0; a < AB; ++a) {
+        ra[a][0] = st.a[AB * wi + a][c0];
+        ra[a][1] = st.a[AB * wi + a][c0 + 16];
+    }
 #pragma unroll
-    for (int b = 0; b < 4; ++b) rns_split(st.b[4 * wj + b][c0], st.b[4 * wj + b][c0 + 16], blo[b], bhi[b]);
-    // dependent MFMAs into md are 16 issues apart
+    for (int b = 0; b < 4; ++b) {
+        rb[b][0] = st.b[4 * wj + b][c0];
+        rb[b][1] = st.b[4 * wj + b][c0 + 16];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    v4i alo[AB], ahi[AB], blo[4], bhi[4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < AB; ++a) rns_split(ra[a][0], ra[a][1], alo[a], ahi[a]);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) rns_split(rb[b][0], rb[b][1], blo[b], bhi[b]);
+    // dependent MFMAs into md are 4 AB issues apart
+#pragma unroll
+    for (int a = 0; a < AB; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
             c.hh[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[a], bhi[b], c.hh[a][b], 0, 0, 0);
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < AB; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
             c.md[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[a], blo[b], c.md[a][b], 0, 0, 0);
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < AB; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
             c.ll[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[a], blo[b], c.ll[a][b], 0, 0, 0);
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < AB; ++a)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
             c.md[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[a], bhi[b], c.md[a][b], 0, 0, 0);
 }
 
-// Workgroup b -> (prime, tile): workgroup b runs on XCD b mod 8; XCD x takes
-// the primes m = x (mod 8), all tiles of one prime after another, so the
-// ~32 workgroups resident on an XCD share one prime's operand panels.
-__global__ __launch_bounds__(256) void k_rns_pointwise(const uint16_t *__restrict__ RA,
-                                                       const uint16_t *__restrict__ RB,
-                                                       const RnsMod *__restrict__ mods, int nm,
-                                                       int np_, uint16_t *__restrict__ Y)
+// Persistent workgroups, one per CU: workgroup b runs on XCD b mod 8 and
+// takes every wx-th (prime, tile) item of its XCD's list (primes m = x mod 8,
+// all tiles of one prime after another), so the wx workgroups of an XCD run
+// one block of BR x BC tiles of one prime at a time and share its operand
+// panels in the XCD's L2.  The copy pipeline runs across tile boundaries:
+// the first k blocks of a workgroup's next tile load while it finishes the
+// current one and writes its results.
+struct TileMap {
+    int tpr, BR, BC;
+    __device__ void tile(int t, int &ti, int &tj) const
+    {
+        const int b = t / (BR * BC), w = t % (BR * BC), nbj = tpr / BC;
+        ti = (b / nbj) * BR + w / BC;
+        tj = (b % nbj) * BC + w % BC;
+    }
+};
+
+template <int AB>
+__global__ __launch_bounds__(64 * 2 * (8 / AB)) void k_rns_pointwise(
+    const uint16_t *__restrict__ RA, const uint16_t *__restrict__ RB,
+    const RnsMod *__restrict__ mods, int nm, int np_, uint16_t *__restrict__ Y, int wx,
+    TileMap tm)
 {
-    __shared__ PwStage s0, s1, s2;
+    constexpr int NW = 2 * (8 / AB);
+    __shared__ PwStage s0, s1, s2, s3;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wi = wave >> 1, wj = wave & 1;
-    const int tpr = np_ / 128, T = tpr * tpr;
-    const int bid = blockIdx.x, xcd = bid & 7, loc = bid >> 3;
-    const int m = (loc / T) * 8 + xcd, tile = loc % T;
-    if (m >= nm) return;
-    const int ti = tile / tpr, tj = tile % tpr;
+    const int T = tm.tpr * tm.tpr, nkb = np_ / 64;
+    const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+    const int items = (nm / 8) * T;          // nm is a multiple of 8
+    const int mine = items > k ? (items - k + wx - 1) / wx : 0;
+    const int G = mine * nkb;                // k-block steps of this workgroup
+    if (G == 0) return;
     const size_t npp = (size_t)np_ * np_, rowb = (size_t)np_ * 2;
-    const char *a0 = (const char *)(RA + m * npp + (size_t)ti * 128 * np_);
-    const char *b0 = (const char *)(RB + m * npp + (size_t)tj * 128 * np_);
     uint32_t off[2];
 #pragma unroll
     for (int sh = 0; sh < 2; ++sh) {
         const int c = 64 * sh + lane;
         off[sh] = (uint32_t)((c & 15) * rowb + (16 * (c >> 5) + 8 * ((c >> 4) & 1)) * 2);
     }
-    PwAcc acc;
+    // item it (of this XCD's list) -> prime and output tile
+    auto decode = [&](int it, int &m, int &ti, int &tj) {
+        m = (it / T) * 8 + xcd;
+        tm.tile(it % T, ti, tj);
+    };
+    // producer cursor: the next block to copy (item p_it, k block p_kb); the
+    // divisions run once per item, not per block
+    const int last_it = k + wx * (mine - 1);
+    int p_it = k, p_kb = 0;
+    const char *pa, *pb;
+    auto panels = [&]() {
+        int m, ti, tj;
+        decode(p_it, m, ti, tj);
+        pa = (const char *)(RA + m * npp + (size_t)ti * 128 * np_);
+        pb = (const char *)(RB + m * npp + (size_t)tj * 128 * np_);
+    };
+    panels();
+    // copy the cursor's block and advance it (past the last block it stays
+    // there: the extra copies repeat the last block)
+    auto issue = [&](PwStage &st) {
+        rns_issue<NW>(st, pa, pb, rowb, p_kb, wave, off);
+        if (++p_kb == nkb) {
+            if (p_it < last_it) {
+                p_kb = 0;
+                p_it += wx;
+                panels();
+            } else {
+                p_kb = nkb - 1;
+            }
+        }
+    };
+    PwAcc<AB> acc;
+    auto zero = [&]() {
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+        for (int a = 0; a < AB; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc.hh[a][b] = acc.md[a][b] = acc.ll[a][b] = v4i{0, 0, 0, 0};
-    const int nkb = np_ / 64;
-    // Every step issues exactly 8 copies per wave (past the last block it
-    // copies the last block again, into the stage just retired), so the
+            for (int b = 0; b < 4; ++b) acc.hh[a][b] = acc.md[a][b] = acc.ll[a][b] = v4i{0, 0, 0, 0};
+    };
+    int c_it = k, c_kb = 0;              // consumer cursor
+    auto epilogue = [&]() {
+        int m, ti, tj;
+        decode(c_it, m, ti, tj);
+        c_it += wx;
+        const RnsMod md = mods[m];
+        uint16_t *y = Y + m * npp;
+#pragma unroll
+        for (int a = 0; a < AB; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int i = ti * 128 + 16 * AB * wi + 16 * a + 4 * (lane >> 4) + v;
+                    const int j = tj * 128 + 64 * wj + 16 * b + (lane & 15);
+                    const double cv = (double)acc.hh[a][b][v] * 65536.0 +
+                                      (double)acc.md[a][b][v] * 256.0 + (double)acc.ll[a][b][v];
+                    // B's residues carry the factor cinv: this is y_m
+                    y[(size_t)i * np_ + j] = rns_pair(rns_reduce(cv, md.p, md.invp));
+                }
+        zero();
+    };
+    zero();
+    // Four stages, three blocks in flight (with two, each block waited
+    // for copies issued only about 1000 MFMA cycles earlier).  Every step
+    // issues exactly 32 / NW copies per wave (past the last step it copies
+    // the last block again, into the stage just retired), so the
     // outstanding copies are the same on every path: the compiler's own
-    // waits then stay at vmcnt(8) (with a conditional issue it waited for
-    // all copies, the ones just issued included, before every block).
-    rns_issue(s0, a0, b0, rowb, 0, wave, off);
-    rns_issue(s1, a0, b0, rowb, min(1, nkb - 1), wave, off);
-    // Stage kb % 3 is complete once this wave's copies of kb are (only those
-    // of kb + 1 may remain: 8 per wave) and every wave has passed the
-    // barrier; the barrier also retires every read of stage (kb + 2) % 3
-    // (block kb - 1), which the copies of kb + 2 then overwrite.
-#define RNS_STEP(S, SN, KB)                                                    \
+    // waits then stay at vmcnt(64 / NW) (with a conditional issue it waited
+    // for all copies, the ones just issued included, before every block).
+    // Stage g % 4 is complete once this wave's copies of g are (only those
+    // of g + 1 and g + 2 may be outstanding after them) and every wave has
+    // passed the barrier; the barrier also retires every read of stage
+    // (g + 3) % 4 (step g - 1), which the copies of g + 3 then overwrite.
+    issue(s0);
+    issue(s1);
+    issue(s2);
+#define RNS_STEP(S, SN, GG)                                                    \
     {                                                                          \
-        wait_vm_lgkm<8>();                                                     \
+        wait_vm_lgkm<64 / NW>();                                               \
         __builtin_amdgcn_s_barrier();                                          \
-        rns_issue(SN, a0, b0, rowb, min((KB) + 2, nkb - 1), wave, off);        \
-        rns_compute(S, wi, wj, lane, acc);                                     \
+        issue(SN);                                                             \
+        rns_compute<AB>(S, wi, wj, lane, acc);                                 \
+        if (++c_kb == nkb) {                                                   \
+            c_kb = 0;                                                          \
+            epilogue();                                                        \
+        }                                                                      \
     }
     // no exits inside the unrolled body: with them the accumulators were
     // copied at every exit and spilled
-    int kb = 0;
+    int g = 0;
 #pragma unroll 1
-    for (; kb + 3 <= nkb; kb += 3) {
-        RNS_STEP(s0, s2, kb)
-        RNS_STEP(s1, s0, kb + 1)
-        RNS_STEP(s2, s1, kb + 2)
+    for (; g + 4 <= G; g += 4) {
+        RNS_STEP(s0, s3, g)
+        RNS_STEP(s1, s0, g + 1)
+        RNS_STEP(s2, s1, g + 2)
+        RNS_STEP(s3, s2, g + 3)
     }
-    if (kb < nkb) RNS_STEP(s0, s2, kb)
-    if (kb + 1 < nkb) RNS_STEP(s1, s0, kb + 1)
+    if (g < G) RNS_STEP(s0, s3, g)
+    if (g + 1 < G) RNS_STEP(s1, s0, g + 1)
+    if (g + 2 < G) RNS_STEP(s2, s1, g + 2)
 #undef RNS_STEP
-    const RnsMod md = mods[m];
-    uint16_t *y = Y + m * npp;
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int i = ti * 128 + 64 * wi + 16 * a + 4 * (lane >> 4) + v;
-                const int j = tj * 128 + 64 * wj + 16 * b + (lane & 15);
-                const double cv = (double)acc.hh[a][b][v] * 65536.0 +
-                                  (double)acc.md[a][b][v] * 256.0 + (double)acc.ll[a][b][v];
-                const int c = rns_reduce(cv, md.p, md.invp);
-                const int yv = rns_reduce((double)c * (double)md.cinv, md.p, md.invp);
-                y[(size_t)i * np_ + j] = rns_pair(yv);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+}
+
+TileMap tile_map(int tpr, int wx)
+{
+    TileMap tm;
+    tm.tpr = tpr;
+    tm.BC = 1;
+    for (int d = 1; d <= 8 && d <= tpr; ++d)
+        if (tpr % d == 0) tm.BC = d;
+    tm.BR = 1;
+    for (int d = 1; d <= wx / tm.BC && d <= tpr; ++d)
+        if (tpr % d == 0) tm.BR = d;
+    return tm;
 }
 
 // ---- 3. CRT and carry ------------------------------------------------------
@@ -350,8 +452,8 @@ __global__ __launch_bounds__(256) void k_rns_pointwise(const uint16_t *__restric
 // workgroup of 8 waves.  LDS: the y digit pairs of the E elements as MFMA B
 // fragments [KBc][EB][64 lanes][16 B] (fragment (kb, cb): element
 // 16 cb + l%16, the digit pairs of primes 32 kb + 8 (l/16) .. +7), the
-// int64 groups [G = Jpad/4][E], q's fp64 sums, and the carry lookahead's run
-// data.  T holds the A fragments [Jpad/16][KBc][64][16 B]: row j (output
+// int64 groups [G = Jpad/4][E], the carry lookahead's run data, and q's
+// partial fp64 sums and values.  T holds the A fragments [Jpad/16][KBc][64][16 B]: row j (output
 // byte) of k = 2m + d is byte j of M/p_m (d = 0) or of 256 M/p_m (d = 1),
 // zero for m >= nm.
 constexpr int kCrtThreads = 512;
@@ -364,66 +466,52 @@ __global__ __launch_bounds__(kCrtThreads) void k_rns_crt(
     uint16_t *__restrict__ out, int RL, int RLc)
 {
     constexpr int NT = kCrtThreads, E = 16 * EB, SEGS = NT / E, NW = NT / 64;
-    constexpr int EG = E / 8, MS = NT / EG;    // groups of 8 elements, prime slots
     extern __shared__ __align__(16) unsigned char smem[];
     v4i *yl = (v4i *)smem;                                        // KBc*EB*64
     long long *grp = (long long *)(yl + (size_t)KBc * EB * 64);  // [G][E]
     const int G = Jpad / 4;
     long long *segc = grp + (size_t)G * E;                        // [SEGS][E] x 4
     long long *seglo = segc + NT, *seghi = seglo + NT, *segin = seghi + NT;
-    double *qs = (double *)(segin + NT);                          // [E]
+    double *qs = (double *)(segin + NT);                          // [NT]
+    long long *qv = (long long *)(qs + NT);                       // [E]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i = blockIdx.y, j0 = blockIdx.x * E;
     const size_t npp = (size_t)np_ * np_, nn = (size_t)n * n;
-    if (tid < E) qs[tid] = 0;
-    __syncthreads();
 
-    // 1. y digit pairs into LDS (16-byte loads of 8 elements of one prime,
-    //    a batch of them in flight per thread), and sum_m y_m / p_m.  Columns
-    //    j0+E <= np; those at or beyond n hold y = 0 (their operand rows
-    //    were zero), so no element needs a check here.
+    // 1. y digit pairs into LDS, and sum_m y_m / p_m.  A thread takes one
+    //    element and groups of 8 primes: 8 loads of one digit pair each
+    //    (each coalesced over the E consecutive elements of the workgroup),
+    //    then one 16-byte write of its fragment slot (lane group pg % 4 of
+    //    k block pg / 4, element e).  Columns at or beyond n hold y = 0
+    //    (their operand rows were zero), so they need no check.
     {
-        const int eg = tid % EG, ms = tid / EG;
-        const uint16_t *src = Y + (size_t)i * np_ + j0 + 8 * eg;
-        uint16_t *yw = (uint16_t *)yl;
-        double qp[8];
+        const int e = tid % E, mg = tid / E;
+        const uint16_t *src = Y + (size_t)i * np_ + j0 + e;
+        double qsum = 0;
+        for (int pg = mg; pg < 4 * KBc; pg += SEGS) {
+            uint32_t w[8];
+            double ip[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) qp[q] = 0;
-        constexpr int BATCH = 8;
-        for (int m0 = ms; m0 < 32 * KBc; m0 += MS * BATCH) {
-            uint4 w[BATCH];
-            double ip[BATCH];
-#pragma unroll
-            for (int b = 0; b < BATCH; ++b) {
-                const int m = m0 + b * MS;
-                if (m < nm) {
-                    w[b] = *(const uint4 *)(src + (size_t)m * npp);
-                    ip[b] = mods[m].invp;
-                } else {
-                    w[b] = uint4{0, 0, 0, 0};
-                    ip[b] = 0;
-                }
+            for (int b = 0; b < 8; ++b) {
+                const int m = 8 * pg + b;
+                w[b] = m < nm ? src[(size_t)m * npp] : 0;
+                ip[b] = m < nm ? mods[m].invp : 0.0;
             }
 #pragma unroll
-            for (int b = 0; b < BATCH; ++b) {
-                const int m = m0 + b * MS;
-                if (m < 32 * KBc) {
-                    const int kb = m >> 5, mq = m & 31;
-                    const uint32_t ww[4] = {w[b].x, w[b].y, w[b].z, w[b].w};
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) {
-                        const uint16_t v = (uint16_t)(ww[q >> 1] >> (16 * (q & 1)));
-                        const int e = 8 * eg + q;
-                        const int ln = (e & 15) + 16 * (mq >> 3);
-                        yw[(((size_t)kb * EB + (e >> 4)) * 64 + ln) * 8 + (mq & 7)] = v;
-                        qp[q] += (double)rns_unpair(v) * ip[b];
-                    }
-                }
-            }
+            for (int b = 0; b < 8; ++b) qsum += (double)rns_unpair((uint16_t)w[b]) * ip[b];
+            const int kb = pg >> 2, ln = (e & 15) + 16 * (pg & 3);
+            yl[((size_t)kb * EB + (e >> 4)) * 64 + ln] =
+                v4i{(int)(w[0] | w[1] << 16), (int)(w[2] | w[3] << 16), (int)(w[4] | w[5] << 16),
+                    (int)(w[6] | w[7] << 16)};
         }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) atomicAdd(&qs[8 * eg + q], qp[q]);
+        qs[tid] = qsum;
+    }
+    __syncthreads();
+    if (tid < E) {
+        double t = 0;
+        for (int r = 0; r < SEGS; ++r) t += qs[r * E + tid];
+        qv[tid] = (long long)rint(t);
     }
     __syncthreads();
 
@@ -477,7 +565,7 @@ __global__ __launch_bounds__(kCrtThreads) void k_rns_crt(
             for (int cb = 0; cb < EB; ++cb) {
                 const int el = 16 * cb + (lane & 15);
                 const int gi = 4 * (4 * ch + jj) + (lane >> 4);
-                const long long q = (long long)rint(qs[el]);
+                const long long q = qv[el];
                 long long g = 0;
 #pragma unroll
                 for (int v = 3; v >= 0; --v)
@@ -557,7 +645,7 @@ __global__ __launch_bounds__(kCrtThreads) void k_rns_crt(
 size_t crt_lds_bytes(int EB, int KBc, int Jpad)
 {
     const int E = 16 * EB;
-    return (size_t)KBc * EB * 1024 + (size_t)(Jpad / 4) * E * 8 + 4 * kCrtThreads * 8 + E * 8;
+    return (size_t)KBc * EB * 1024 + (size_t)(Jpad / 4) * E * 8 + 5 * kCrtThreads * 8 + E * 8;
 }
 
 // ---- host planning ---------------------------------------------------------
@@ -633,10 +721,11 @@ int kres_blocks(int L)
 
 struct mfh_rns {
     int n, np, L, nm, nmk, KB, Jpad, crt_eb;
+    int cus;              // compute units (8 XCDs of cus / 8)
     int dev;
     hipStream_t stream;
     RnsMod *dMod;
-    v4i *dW, *dT;
+    v4i *dW, *dWb, *dT;
     int8_t *dMb;
     uint16_t *dRA, *dRB, *dY, *dBt;
     size_t bytes;
@@ -656,45 +745,15 @@ int rns_alloc(mfh_rns *r, void **p, size_t bytes)
     return MFH_OK;
 }
 
-// weight fragments of the residue GEMM and the CRT tables
+// weight fragments of the residue GEMM (plain, and times cinv for B) and the
+// CRT tables
 int rns_tables(mfh_rns *r)
 {
     const int nm = r->nm, L = r->L, KB = r->KB, Jpad = r->Jpad, nmk = r->nmk;
     const int KBc = nmk / 32;
     std::vector<RnsMod> mods(nm);
-    // residue weights: [nm/8][KB][64][16]
-    std::vector<int8_t> W((size_t)(nm / 8) * KB * 1024, 0);
-    std::vector<int8_t> wlo((size_t)2 * L), whi((size_t)2 * L);
-    for (int m = 0; m < nm; ++m) {
-        const long long p = r->primes[m];
-        long long w = 1, s1 = 0;
-        for (int t = 0; t < 2 * L; ++t) {
-            const long long wb = w > p / 2 ? w - p : w;
-            const long long lo = ((wb + 128) & 255) - 128;
-            wlo[t] = (int8_t)lo;
-            whi[t] = (int8_t)((wb - lo) / 256);
-            s1 = (s1 + w) % p;
-            w = w * 256 % p;
-        }
-        const long long k0 = 128 * s1 % p;              // 128 sum_t 256^t
-        const long long k1 = ((k0 - w) % p + p) % p;    // w = 2^W mod p now
-        mods[m].p = (int)p;
-        mods[m].k0 = (int)k0;
-        mods[m].k1 = (int)k1;
-        mods[m].invp = 1.0 / (double)p;
-        for (int d = 0; d < 2; ++d) {
-            const int o = 2 * m + d, ob = o / 16, row = o % 16;
-            for (int kb = 0; kb < KB; ++kb)
-                for (int g = 0; g < 4; ++g)
-                    for (int b = 0; b < 16; ++b) {
-                        const int t = 64 * kb + 16 * g + b;
-                        if (t >= 2 * L) continue;
-                        const int ln = row + 16 * g;
-                        W[(((size_t)ob * KB + kb) * 64 + ln) * 16 + b] = d ? whi[t] : wlo[t];
-                    }
-        }
-    }
-    // M and M/p_m
+    // M and, per prime, cinv = (M/p_m)^-1 mod p_m, (M/p_m) mod p_m being
+    // prod_{j != m} p_j mod p_m
     std::vector<uint32_t> M(1, 1);
     for (int m = 0; m < nm; ++m) {
         uint64_t c = 0;
@@ -705,6 +764,45 @@ int rns_tables(mfh_rns *r)
         }
         if (c) M.push_back((uint32_t)c);
     }
+    for (int m = 0; m < nm; ++m) {
+        const long long p = r->primes[m];
+        long long pr = 1;
+        for (int j = 0; j < nm; ++j)
+            if (j != m) pr = pr * (r->primes[j] % p) % p;
+        mods[m].cinv = (int)modinv(pr, p);
+    }
+    // residue weights: [nm/8][KB][64][16], w_t = 256^t mod p (W) and
+    // w_t cinv mod p (Wb), each as two balanced base-2^8 digits
+    std::vector<int8_t> W((size_t)(nm / 8) * KB * 1024, 0), Wb(W.size(), 0);
+    auto put = [&](std::vector<int8_t> &dst, int m, int t, long long w, long long p) {
+        const long long wb = w > p / 2 ? w - p : w;
+        const long long lo = ((wb + 128) & 255) - 128;
+        const long long hi = (wb - lo) / 256;
+        for (int d = 0; d < 2; ++d) {
+            const int o = 2 * m + d, ob = o / 16, row = o % 16;
+            const int kb = t / 64, g = (t % 64) / 16, b = t % 16;
+            dst[(((size_t)ob * KB + kb) * 64 + row + 16 * g) * 16 + b] = (int8_t)(d ? hi : lo);
+        }
+    };
+    for (int m = 0; m < nm; ++m) {
+        const long long p = r->primes[m], ci = mods[m].cinv;
+        long long w = 1, s1 = 0;
+        for (int t = 0; t < 2 * L; ++t) {
+            put(W, m, t, w, p);
+            put(Wb, m, t, w * ci % p, p);
+            s1 = (s1 + w) % p;
+            w = w * 256 % p;
+        }
+        const long long k0 = 128 * s1 % p;              // 128 sum_t 256^t
+        const long long k1 = ((k0 - w) % p + p) % p;    // w = 2^W mod p now
+        mods[m].p = (int)p;
+        mods[m].k0 = (int)k0;
+        mods[m].k1 = (int)k1;
+        mods[m].k0b = (int)(k0 * ci % p);
+        mods[m].k1b = (int)(k1 * ci % p);
+        mods[m].invp = 1.0 / (double)p;
+    }
+    // CRT: the balanced bytes of M and of each M/p_m
     std::vector<int8_t> mbh(Jpad);
     balanced_bytes(M, Jpad, mbh.data());
     std::vector<int8_t> T((size_t)(Jpad / 16) * KBc * 1024, 0);
@@ -718,11 +816,6 @@ int rns_tables(mfh_rns *r)
             Mm[w] = (uint32_t)(cur / p);
             rem = cur % p;
         }
-        // (M/p_m) mod p_m = prod_{j != m} p_j mod p_m
-        long long pr = 1;
-        for (int j = 0; j < nm; ++j)
-            if (j != m) pr = pr * (r->primes[j] % (long long)p) % (long long)p;
-        mods[m].cinv = (int)modinv(pr, (long long)p);
         balanced_bytes(Mm, Jpad, dm.data());
         for (int d = 0; d < 2; ++d) {
             const int k = 2 * m + d, kb = k / 64, g = (k % 64) / 16, b = k % 16;
@@ -735,33 +828,38 @@ int rns_tables(mfh_rns *r)
     }
     int rc = rns_alloc(r, (void **)&r->dMod, mods.size() * sizeof(RnsMod));
     if (!rc) rc = rns_alloc(r, (void **)&r->dW, W.size());
+    if (!rc) rc = rns_alloc(r, (void **)&r->dWb, Wb.size());
     if (!rc) rc = rns_alloc(r, (void **)&r->dT, T.size());
     if (!rc) rc = rns_alloc(r, (void **)&r->dMb, mbh.size());
     if (rc) return rc;
     MFH_HIP(hipMemcpy(r->dMod, mods.data(), mods.size() * sizeof(RnsMod), hipMemcpyHostToDevice));
     MFH_HIP(hipMemcpy(r->dW, W.data(), W.size(), hipMemcpyHostToDevice));
+    MFH_HIP(hipMemcpy(r->dWb, Wb.data(), Wb.size(), hipMemcpyHostToDevice));
     MFH_HIP(hipMemcpy(r->dT, T.data(), T.size(), hipMemcpyHostToDevice));
     MFH_HIP(hipMemcpy(r->dMb, mbh.data(), mbh.size(), hipMemcpyHostToDevice));
     return MFH_OK;
 }
 
 template <int KB, int EB>
-void launch_residue(const mfh_rns *r, const uint16_t *X, int sgn, uint16_t *R)
+void launch_residue(const mfh_rns *r, const uint16_t *X, int sgn, int scaled, uint16_t *R)
 {
     // a workgroup covers 4 waves x 16 EB consecutive elements of one row
     dim3 grid((r->np + 64 * EB - 1) / (64 * EB), r->np);
     hipLaunchKernelGGL((k_rns_residue<KB, EB>), grid, dim3(256), 0, r->stream, X, r->n, r->np,
-                       r->L, sgn, (const v4i *)r->dW, (const RnsMod *)r->dMod, r->nm, R);
+                       r->L, sgn, scaled, (const v4i *)(scaled ? r->dWb : r->dW),
+                       (const RnsMod *)r->dMod, r->nm, R);
 }
 
-int run_residue(const mfh_rns *r, const uint16_t *X, int sgn, uint16_t *R)
+int run_residue(const mfh_rns *r, const uint16_t *X, int sgn, int scaled, uint16_t *R)
 {
     switch (r->KB) {
-    case 1: launch_residue<1, 4>(r, X, sgn, R); break;
-    case 2: launch_residue<2, 4>(r, X, sgn, R); break;
-    case 4: launch_residue<4, 4>(r, X, sgn, R); break;
-    case 8: launch_residue<8, 4>(r, X, sgn, R); break;
-    case 16: launch_residue<16, 2>(r, X, sgn, R); break;
+    // EB = 4 element blocks per wave (EB = 8 for L <= 128 left one wave per
+    // SIMD and ran 35 % slower: the limb loads need the occupancy)
+    case 1: launch_residue<1, 4>(r, X, sgn, scaled, R); break;
+    case 2: launch_residue<2, 4>(r, X, sgn, scaled, R); break;
+    case 4: launch_residue<4, 4>(r, X, sgn, scaled, R); break;
+    case 8: launch_residue<8, 4>(r, X, sgn, scaled, R); break;
+    case 16: launch_residue<16, 2>(r, X, sgn, scaled, R); break;
     default: return MFH_E_BOUND;
     }
     MFH_HIP(hipGetLastError());
@@ -822,6 +920,7 @@ int mfh_rns_create(mfh_rns **out, int n, int L)
         strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return MFH_E_NODEV;
     mfh_rns *r = new mfh_rns();
+    r->cus = prop.multiProcessorCount >= 8 ? prop.multiProcessorCount / 8 * 8 : 8;
     r->n = n;
     r->L = L;
     r->np = (n + 127) / 128 * 128;
@@ -856,7 +955,7 @@ void mfh_rns_destroy(mfh_rns *r)
 {
     if (!r) return;
     if (r->stream) (void)hipStreamSynchronize(r->stream);
-    void *bufs[] = {r->dMod, r->dW, r->dT, r->dMb, r->dRA, r->dRB, r->dY, r->dBt};
+    void *bufs[] = {r->dMod, r->dW, r->dWb, r->dT, r->dMb, r->dRA, r->dRB, r->dY, r->dBt};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     for (auto &e : r->ev)
@@ -878,7 +977,7 @@ int mfh_rns_residues_dev(mfh_rns *r, int in_kind, const void *dX, void *dR)
 {
     if (!r || !dX || !dR) return MFH_E_ARG;
     if (in_kind != MFH_IN_U16 && in_kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
-    return run_residue(r, (const uint16_t *)dX, in_kind == MFH_IN_U16_SIGNED, (uint16_t *)dR);
+    return run_residue(r, (const uint16_t *)dX, in_kind == MFH_IN_U16_SIGNED, 0, (uint16_t *)dR);
 }
 
 int mfh_rns_mm_dev(mfh_rns *r, int in_kind, const void *dA, const void *dB, void *dOut, int RL)
@@ -888,14 +987,17 @@ int mfh_rns_mm_dev(mfh_rns *r, int in_kind, const void *dA, const void *dB, void
     const int sgn = in_kind == MFH_IN_U16_SIGNED;
     rns_mark(r, 0);
     int rc = mfh_launch_transpose(dB, r->dBt, r->L, r->n, 2, r->stream);
-    if (!rc) rc = run_residue(r, (const uint16_t *)dA, sgn, r->dRA);
-    if (!rc) rc = run_residue(r, r->dBt, sgn, r->dRB);
+    if (!rc) rc = run_residue(r, (const uint16_t *)dA, sgn, 0, r->dRA);
+    if (!rc) rc = run_residue(r, r->dBt, sgn, 1, r->dRB);
     if (rc) return rc;
     rns_mark(r, 1);
-    const int T = (r->np / 128) * (r->np / 128);
-    hipLaunchKernelGGL(k_rns_pointwise, dim3(r->nm * T), dim3(256), 0, r->stream,
+    const int wx = r->cus / 8;               // persistent workgroups per XCD
+    // eight waves of 32 x 64 (two per SIMD); four waves of 64 x 64 spilled
+    // and ran 1.8x slower
+    hipLaunchKernelGGL(k_rns_pointwise<2>, dim3(8 * wx), dim3(512), 0, r->stream,
                        (const uint16_t *)r->dRA, (const uint16_t *)r->dRB,
-                       (const RnsMod *)r->dMod, r->nm, r->np, r->dY);
+                       (const RnsMod *)r->dMod, r->nm, r->np, r->dY, wx,
+                       tile_map(r->np / 128, wx));
     MFH_HIP(hipGetLastError());
     rns_mark(r, 2);
     const int RLc = std::min(RL, 2 * r->L + 1);
