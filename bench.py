@@ -8,8 +8,11 @@ generated on the device bit-identically to the reference's bigmat_rand).
 
 Prints ONE JSON line.  `value` is ms per product (lower is better); the line
 also carries the issued int8 TOPS, the pointwise kernel's fraction of the
-int8 MFMA peak (`roofline`), and the reference CPU path timed on a bounded
-sample on this host (`cpu_baseline`).
+int8 MFMA peak (`roofline`), the reference CPU path timed on a bounded
+sample on this host (`cpu_baseline`), and, in `multimodular`, the same
+product computed by residue number system arithmetic (mfh_rns_mm_dev, no
+reference counterpart) on the same inputs, with whether its limbs equal the
+MFFT product's.
 """
 import argparse
 import ctypes as C
@@ -245,7 +248,9 @@ def method_table(args):
     speedup baseline as in src/main.c:293-297), the flat MFFT plan and the
     recursive plan (and, at K = 16, the flat plan with the K^2-product
     pointwise kernel forced); limbplane-mma is the schoolbook on the int8
-    matrix cores.  `products` is each method's n x n product
+    matrix cores; rns is the multi-modular product (no reference
+    counterpart: its `products` count the primes, each 4 int8 GEMMs).
+    `products` is each method's n x n product
     count as the reference defines it (mfft_plan.nprod); `issued` is the
     ring products the device issued (NB times the per-point count of
     mfh_pointwise_info; each is 6 or 9 int8 digit GEMMs); `kernel_calls` is

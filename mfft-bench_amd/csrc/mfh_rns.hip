@@ -456,16 +456,16 @@ TileMap tile_map(int tpr, int wx)
 // partial fp64 sums and values.  T holds the A fragments [Jpad/16][KBc][64][16 B]: row j (output
 // byte) of k = 2m + d is byte j of M/p_m (d = 0) or of 256 M/p_m (d = 1),
 // zero for m >= nm.
-constexpr int kCrtThreads = 512;
-constexpr int kCrtBatch = 4;       // k blocks of T fragments loaded at once
-
-template <int EB>
-__global__ __launch_bounds__(kCrtThreads) void k_rns_crt(
+// NT threads (512, or 256 for narrow outputs of at most four chunks);
+// KBB: the T fragments of a chunk are loaded in batches of KBB k blocks,
+// double-buffered (DBL), or all at once (KBB >= KBc, one wait per chunk)
+template <int EB, int NT, int KBB, bool DBL>
+__global__ __launch_bounds__(NT) void k_rns_crt(
     const uint16_t *__restrict__ Y, int n, int np_, int nm, int KBc, int Jpad,
     const v4i *__restrict__ T, const int8_t *__restrict__ mb, const RnsMod *__restrict__ mods,
     uint16_t *__restrict__ out, int RL, int RLc)
 {
-    constexpr int NT = kCrtThreads, E = 16 * EB, SEGS = NT / E, NW = NT / 64;
+    constexpr int E = 16 * EB, SEGS = NT / E, NW = NT / 64;
     extern __shared__ __align__(16) unsigned char smem[];
     v4i *yl = (v4i *)smem;                                        // KBc*EB*64
     long long *grp = (long long *)(yl + (size_t)KBc * EB * 64);  // [G][E]
@@ -517,8 +517,9 @@ __global__ __launch_bounds__(kCrtThreads) void k_rns_crt(
 
     // 2. byte columns: GEMM over the y digits, q M subtracted, groups of 4.
     //    A wave takes chunks of 64 output bytes (4 fragment rows); the T
-    //    fragments of a chunk stream in batches of kCrtBatch k blocks, the
-    //    next batch loaded while the current one is multiplied.
+    //    fragments of a chunk stream in batches of KBB k blocks, the next
+    //    batch loaded while the current one is multiplied (DBL), or arrive
+    //    all at once.
     const int nch = Jpad / 64;
     for (int ch = wave; ch < nch; ch += NW) {
         v4i acc[4][EB];
@@ -527,18 +528,18 @@ __global__ __launch_bounds__(kCrtThreads) void k_rns_crt(
 #pragma unroll
             for (int cb = 0; cb < EB; ++cb) acc[jj][cb] = v4i{0, 0, 0, 0};
         const v4i *tp = T + (size_t)4 * ch * KBc * 64 + lane;
-        v4i ta[kCrtBatch][4], tb[kCrtBatch][4];
-        auto load = [&](v4i (&t)[kCrtBatch][4], int kb0) {
+        v4i ta[KBB][4], tb[DBL ? KBB : 1][4];
+        auto load = [&](v4i (&t)[KBB][4], int kb0) {
 #pragma unroll
-            for (int b = 0; b < kCrtBatch; ++b)
+            for (int b = 0; b < KBB; ++b)
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
                     t[b][jj] = kb0 + b < KBc ? tp[((size_t)jj * KBc + kb0 + b) * 64]
                                              : v4i{0, 0, 0, 0};
         };
-        auto mul = [&](const v4i (&t)[kCrtBatch][4], int kb0) {
+        auto mul = [&](const v4i (&t)[KBB][4], int kb0) {
 #pragma unroll
-            for (int b = 0; b < kCrtBatch; ++b) {
+            for (int b = 0; b < KBB; ++b) {
                 if (kb0 + b >= KBc) continue;
                 v4i yf[EB];
 #pragma unroll
@@ -553,11 +554,15 @@ __global__ __launch_bounds__(kCrtThreads) void k_rns_crt(
             }
         };
         load(ta, 0);
-        for (int kb0 = 0; kb0 < KBc; kb0 += 2 * kCrtBatch) {
-            load(tb, kb0 + kCrtBatch);
-            mul(ta, kb0);
-            load(ta, kb0 + 2 * kCrtBatch);
-            mul(tb, kb0 + kCrtBatch);
+        if constexpr (DBL) {
+            for (int kb0 = 0; kb0 < KBc; kb0 += 2 * KBB) {
+                load(tb, kb0 + KBB);
+                mul(ta, kb0);
+                load(ta, kb0 + 2 * KBB);
+                mul(tb, kb0 + KBB);
+            }
+        } else {
+            mul(ta, 0);
         }
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj)
@@ -642,10 +647,10 @@ __global__ __launch_bounds__(kCrtThreads) void k_rns_crt(
     }
 }
 
-size_t crt_lds_bytes(int EB, int KBc, int Jpad)
+size_t crt_lds_bytes(int EB, int NT, int KBc, int Jpad)
 {
     const int E = 16 * EB;
-    return (size_t)KBc * EB * 1024 + (size_t)(Jpad / 4) * E * 8 + 5 * kCrtThreads * 8 + E * 8;
+    return (size_t)KBc * EB * 1024 + (size_t)(Jpad / 4) * E * 8 + 5 * NT * 8 + E * 8;
 }
 
 // ---- host planning ---------------------------------------------------------
@@ -866,23 +871,44 @@ int run_residue(const mfh_rns *r, const uint16_t *X, int sgn, int scaled, uint16
     return MFH_OK;
 }
 
-template <int EB>
+template <int EB, int NT, int KBB, bool DBL>
 int launch_crt(const mfh_rns *r, uint16_t *out, int RL, int RLc)
 {
     const int KBc = r->nmk / 32;
-    const size_t lds = crt_lds_bytes(EB, KBc, r->Jpad);
+    const size_t lds = crt_lds_bytes(EB, NT, KBc, r->Jpad);
     static bool attr_set = false;
     if (!attr_set) {
-        MFH_HIP(hipFuncSetAttribute((const void *)k_rns_crt<EB>,
+        MFH_HIP(hipFuncSetAttribute((const void *)k_rns_crt<EB, NT, KBB, DBL>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         attr_set = true;
     }
     dim3 grid((r->n + 16 * EB - 1) / (16 * EB), r->n);
-    hipLaunchKernelGGL((k_rns_crt<EB>), grid, dim3(kCrtThreads), lds, r->stream, r->dY, r->n, r->np,
-                       r->nm, KBc, r->Jpad, (const v4i *)r->dT, r->dMb, (const RnsMod *)r->dMod,
-                       out, RL, RLc);
+    hipLaunchKernelGGL((k_rns_crt<EB, NT, KBB, DBL>), grid, dim3(NT), lds, r->stream, r->dY,
+                       r->n, r->np, r->nm, KBc, r->Jpad, (const v4i *)r->dT, r->dMb,
+                       (const RnsMod *)r->dMod, out, RL, RLc);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
+}
+
+// the CRT kernel's shape: at most four output chunks: 4 waves; T fragments
+// of at most 9 k blocks in one batch, else batches of 4, double-buffered
+int run_crt(const mfh_rns *r, uint16_t *out, int RL, int RLc)
+{
+    const int KBc = r->nmk / 32, nch = r->Jpad / 64;
+    const bool narrow = nch <= 4, one = KBc <= 9;
+    switch (r->crt_eb) {
+    case 4:
+        if (narrow) return one ? launch_crt<4, 256, 9, false>(r, out, RL, RLc)
+                               : launch_crt<4, 256, 4, true>(r, out, RL, RLc);
+        return one ? launch_crt<4, 512, 9, false>(r, out, RL, RLc)
+                   : launch_crt<4, 512, 4, true>(r, out, RL, RLc);
+    case 2:
+        return one ? launch_crt<2, 512, 9, false>(r, out, RL, RLc)
+                   : launch_crt<2, 512, 4, true>(r, out, RL, RLc);
+    default:
+        return one ? launch_crt<1, 512, 9, false>(r, out, RL, RLc)
+                   : launch_crt<1, 512, 4, true>(r, out, RL, RLc);
+    }
 }
 
 void rns_mark(mfh_rns *r, int k)
@@ -932,7 +958,7 @@ int mfh_rns_create(mfh_rns **out, int n, int L)
     r->Jpad = (2 * (2 * L + 1) + 63) / 64 * 64;
     r->crt_eb = 0;
     for (int eb : {4, 2, 1})
-        if (crt_lds_bytes(eb, r->nmk / 32, r->Jpad) <= 150 * 1024) { r->crt_eb = eb; break; }
+        if (crt_lds_bytes(eb, 512, r->nmk / 32, r->Jpad) <= 150 * 1024) { r->crt_eb = eb; break; }
     if (!r->crt_eb) { delete r; return MFH_E_BOUND; }
     r->dev = 0;
     if (hipSetDevice(0) != hipSuccess || hipStreamCreate(&r->stream) != hipSuccess) {
@@ -1001,11 +1027,7 @@ int mfh_rns_mm_dev(mfh_rns *r, int in_kind, const void *dA, const void *dB, void
     MFH_HIP(hipGetLastError());
     rns_mark(r, 2);
     const int RLc = std::min(RL, 2 * r->L + 1);
-    switch (r->crt_eb) {
-    case 4: rc = launch_crt<4>(r, (uint16_t *)dOut, RL, RLc); break;
-    case 2: rc = launch_crt<2>(r, (uint16_t *)dOut, RL, RLc); break;
-    default: rc = launch_crt<1>(r, (uint16_t *)dOut, RL, RLc); break;
-    }
+    rc = run_crt(r, (uint16_t *)dOut, RL, RLc);
     if (rc) return rc;
     rns_mark(r, 3);
     return MFH_OK;

@@ -49,3 +49,43 @@ def test_rns_limits(lib):
     assert lib.mfh_rns_create(C.byref(h), 32769, 8) == -4
     assert lib.mfh_rns_create(C.byref(h), 16, 513) == -4
     assert lib.mfh_rns_primes(0, 8, None, 0) == -3
+
+
+def test_digit_pair_packing():
+    """the stored digit pair of a balanced residue r is (r + 128) ^ 0x80 in
+    16 bits: low byte lo = ((r+128) & 255) - 128 and high byte
+    hi = (r - lo) / 256, both int8, with r = 256 hi + lo"""
+    import numpy as np
+    r = np.arange(-32639, 32640, dtype=np.int64)
+    w = ((r + 128) ^ 0x80) & 0xFFFF
+    lo = (w & 255).astype(np.int64)
+    hi = (w >> 8).astype(np.int64)
+    lo = np.where(lo >= 128, lo - 256, lo)
+    hi = np.where(hi >= 128, hi - 256, hi)
+    assert np.array_equal(256 * hi + lo, r)
+    assert hi.min() >= -128 and hi.max() <= 127
+
+
+def test_fp64_reduction_needs_no_fixup(lib):
+    """q = rint(v * fl(1/p)), r = v - q p (the kernels' reduction, in IEEE
+    float64 as on the device) gives the balanced residue, |r| <= (p-1)/2,
+    for |v| <= 2^46: v * fl(1/p) is within 2^-22 of v/p, and v/p is never
+    closer than 1/(2p) to a half-integer.  Checked at the points closest to
+    the half-integers (v = k p + (p-1)/2 and k p - (p-1)/2) and at random v,
+    for the largest and smallest primes of the plans."""
+    import numpy as np
+    import mfft_ctypes
+    ps = list(mfft_ctypes.rns_primes(256, 512))
+    rng = np.random.default_rng(5)
+    for p in (int(ps[0]), int(ps[-1]), 65269, 16411):
+        h = (p - 1) // 2
+        k = rng.integers(-(1 << 46) // p, (1 << 46) // p, size=20000, dtype=np.int64)
+        v = np.concatenate([k * p + h, k * p - h, k * p,
+                            rng.integers(-(1 << 46), 1 << 46, size=20000, dtype=np.int64)])
+        v = v[np.abs(v) <= (1 << 46)]
+        vd = v.astype(np.float64)
+        assert np.array_equal(vd.astype(np.int64), v)            # exact in fp64
+        q = np.rint(vd * (1.0 / p))
+        r = (v - q.astype(np.int64) * p)
+        assert np.abs(r).max() <= h, p
+        assert np.array_equal(np.mod(r - v, p), np.zeros_like(r))
