@@ -103,8 +103,9 @@ __device__ __forceinline__ void wait_vm_lgkm()
 // planes of np x np (row stride np), zero outside n x n.  A wave owns EB
 // blocks of 16 consecutive k of row r = blockIdx.y and keeps their byte
 // fragments of all KB 64-byte k blocks in registers; W holds the weight
-// fragments [nm/8][KB][64 lanes][16 B]: fragment (ob, kb) row o = 16 ob + l%16
-// is digit o%2 (0: lo, 1: hi) of w_{8 ob + o/2, t}, t = 64 kb + byte.
+// fragments [ceil(nm/8)][KB][64 lanes][16 B]: fragment (ob, kb) row
+// o = 16 ob + l%16 is digit o%2 (0: lo, 1: hi) of w_{8 ob + o/2, t},
+// t = 64 kb + byte (zero past the last prime).
 // scaled: W holds the weights times cinv (B's residues, so that the
 // per-prime products come out already multiplied by cinv), with the offsets
 // k0b / k1b
@@ -155,15 +156,16 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
     v4i wn[PF > 0 ? PF : 1];
 #pragma unroll
     for (int kb = 0; kb < PF; ++kb) wn[kb] = W[(size_t)kb * 64 + lane];
+    const int nob = (nm + 7) / 8;            // blocks of 8 primes, the last partial
 #pragma unroll 1
-    for (int ob = 0; ob < nm / 8; ++ob) {
+    for (int ob = 0; ob < nob; ++ob) {
         v4i acc[EB];
 #pragma unroll
         for (int cb = 0; cb < EB; ++cb) acc[cb] = v4i{0, 0, 0, 0};
         v4i wc[PF > 0 ? PF : 1];
 #pragma unroll
         for (int kb = 0; kb < PF; ++kb) wc[kb] = wn[kb];
-        if (PF && ob + 1 < nm / 8) {
+        if (PF && ob + 1 < nob) {
 #pragma unroll
             for (int kb = 0; kb < PF; ++kb) wn[kb] = W[((size_t)(ob + 1) * KB + kb) * 64 + lane];
         }
@@ -177,6 +179,7 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm) {
             const int m = 8 * ob + 2 * grp + mm;
+            if (m >= nm) continue;               // zero weights past the last prime
             const RnsMod md = mods[m];
             uint16_t *dst = R + (size_t)m * npp + (size_t)r * np_;
 #pragma unroll
@@ -293,10 +296,12 @@ __device__ __forceinline__ void rns_compute(const PwStage &st, int wi, int wj, i
 }
 
 // Persistent workgroups, one per CU: workgroup b runs on XCD b mod 8 and
-// takes every wx-th (prime, tile) item of its XCD's list (primes m = x mod 8,
-// all tiles of one prime after another), so the wx workgroups of an XCD run
-// one block of BR x BC tiles of one prime at a time and share its operand
-// panels in the XCD's L2.  The copy pipeline runs across tile boundaries:
+// takes every wx-th (prime, tile) item of its XCD's range of the list (all
+// tiles of one prime after another; XCD x gets the R items from x R, R a
+// multiple of the BR x BC block), so the wx workgroups of an XCD run one
+// block of BR x BC tiles of one prime at a time and share its operand panels
+// in the XCD's L2, and the XCDs get equal shares of the work whatever the
+// number of primes.  The copy pipeline runs across tile boundaries:
 // the first k blocks of a workgroup's next tile load while it finishes the
 // current one and writes its results.
 struct TileMap {
@@ -313,7 +318,7 @@ template <int AB>
 __global__ __launch_bounds__(64 * 2 * (8 / AB)) void k_rns_pointwise(
     const uint16_t *__restrict__ RA, const uint16_t *__restrict__ RB,
     const RnsMod *__restrict__ mods, int nm, int np_, uint16_t *__restrict__ Y, int wx,
-    TileMap tm)
+    TileMap tm, int R)
 {
     constexpr int NW = 2 * (8 / AB);
     __shared__ PwStage s0, s1, s2, s3;
@@ -321,7 +326,9 @@ __global__ __launch_bounds__(64 * 2 * (8 / AB)) void k_rns_pointwise(
     const int wi = wave >> 1, wj = wave & 1;
     const int T = tm.tpr * tm.tpr, nkb = np_ / 64;
     const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
-    const int items = (nm / 8) * T;          // nm is a multiple of 8
+    // this XCD's items: [lo, hi) of the (prime, tile) list, prime-major
+    const int N = nm * T, lo = min(xcd * R, N), hi = min(lo + R, N);
+    const int items = hi - lo;
     const int mine = items > k ? (items - k + wx - 1) / wx : 0;
     const int G = mine * nkb;                // k-block steps of this workgroup
     if (G == 0) return;
@@ -332,15 +339,15 @@ __global__ __launch_bounds__(64 * 2 * (8 / AB)) void k_rns_pointwise(
         const int c = 64 * sh + lane;
         off[sh] = (uint32_t)((c & 15) * rowb + (16 * (c >> 5) + 8 * ((c >> 4) & 1)) * 2);
     }
-    // item it (of this XCD's list) -> prime and output tile
+    // item it -> prime and output tile
     auto decode = [&](int it, int &m, int &ti, int &tj) {
-        m = (it / T) * 8 + xcd;
+        m = it / T;
         tm.tile(it % T, ti, tj);
     };
     // producer cursor: the next block to copy (item p_it, k block p_kb); the
     // divisions run once per item, not per block
-    const int last_it = k + wx * (mine - 1);
-    int p_it = k, p_kb = 0;
+    const int last_it = lo + k + wx * (mine - 1);
+    int p_it = lo + k, p_kb = 0;
     const char *pa, *pb;
     auto panels = [&]() {
         int m, ti, tj;
@@ -370,7 +377,7 @@ __global__ __launch_bounds__(64 * 2 * (8 / AB)) void k_rns_pointwise(
 #pragma unroll
             for (int b = 0; b < 4; ++b) acc.hh[a][b] = acc.md[a][b] = acc.ll[a][b] = v4i{0, 0, 0, 0};
     };
-    int c_it = k, c_kb = 0;              // consumer cursor
+    int c_it = lo + k, c_kb = 0;         // consumer cursor
     auto epilogue = [&]() {
         int m, ti, tj;
         decode(c_it, m, ti, tj);
@@ -670,7 +677,7 @@ const std::vector<int> &prime_list()
 }
 
 // the primes of a plan: the largest ones until sum log2 p >= 2W + ceil(log2 n)
-// + 3 (M > 4 n 2^(2W) with a bit to spare), then up to a multiple of 8
+// + 3 (M > 4 n 2^(2W) with a bit to spare)
 int plan_primes(int n, int L, std::vector<int> &ps)
 {
     ps.clear();
@@ -680,12 +687,12 @@ int plan_primes(int n, int L, std::vector<int> &ps)
     const std::vector<int> &pr = prime_list();
     double bits = 0;
     size_t k = 0;
-    while (k < pr.size() && (bits < need || ps.size() % 8)) {
+    while (k < pr.size() && bits < need) {
         ps.push_back(pr[k]);
         bits += log2((double)pr[k]);
         ++k;
     }
-    if (bits < need || ps.size() % 8) return MFH_E_BOUND;
+    if (bits < need) return MFH_E_BOUND;
     return MFH_OK;
 }
 
@@ -776,9 +783,9 @@ int rns_tables(mfh_rns *r)
             if (j != m) pr = pr * (r->primes[j] % p) % p;
         mods[m].cinv = (int)modinv(pr, p);
     }
-    // residue weights: [nm/8][KB][64][16], w_t = 256^t mod p (W) and
+    // residue weights: [ceil(nm/8)][KB][64][16], w_t = 256^t mod p (W) and
     // w_t cinv mod p (Wb), each as two balanced base-2^8 digits
-    std::vector<int8_t> W((size_t)(nm / 8) * KB * 1024, 0), Wb(W.size(), 0);
+    std::vector<int8_t> W((size_t)((nm + 7) / 8) * KB * 1024, 0), Wb(W.size(), 0);
     auto put = [&](std::vector<int8_t> &dst, int m, int t, long long w, long long p) {
         const long long wb = w > p / 2 ? w - p : w;
         const long long lo = ((wb + 128) & 255) - 128;
@@ -1020,10 +1027,12 @@ int mfh_rns_mm_dev(mfh_rns *r, int in_kind, const void *dA, const void *dB, void
     const int wx = r->cus / 8;               // persistent workgroups per XCD
     // eight waves of 32 x 64 (two per SIMD); four waves of 64 x 64 spilled
     // and ran 1.8x slower
+    const TileMap tm = tile_map(r->np / 128, wx);
+    const int N = r->nm * tm.tpr * tm.tpr, blk = tm.BR * tm.BC;
+    const int R = ((N + 7) / 8 + blk - 1) / blk * blk;
     hipLaunchKernelGGL(k_rns_pointwise<2>, dim3(8 * wx), dim3(512), 0, r->stream,
                        (const uint16_t *)r->dRA, (const uint16_t *)r->dRB,
-                       (const RnsMod *)r->dMod, r->nm, r->np, r->dY, wx,
-                       tile_map(r->np / 128, wx));
+                       (const RnsMod *)r->dMod, r->nm, r->np, r->dY, wx, tm, R);
     MFH_HIP(hipGetLastError());
     rns_mark(r, 2);
     const int RLc = std::min(RL, 2 * r->L + 1);

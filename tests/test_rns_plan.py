@@ -21,7 +21,6 @@ def is_prime(p):
 def test_rns_primes_bound(lib, n, L):
     import mfft_ctypes
     ps = [int(p) for p in mfft_ctypes.rns_primes(n, L)]
-    assert len(ps) % 8 == 0
     assert len(set(ps)) == len(ps)
     assert ps == sorted(ps, reverse=True)
     assert all(is_prime(p) and p <= 65279 for p in ps)
@@ -30,16 +29,17 @@ def test_rns_primes_bound(lib, n, L):
     M = math.prod(ps)
     W = 16 * L
     assert M > 4 * n * (1 << (2 * W)), "reconstruction margin"
-    # no prime more than the bound and the rounding to 8 need
-    assert math.prod(ps[:-8]) <= 4 * n * (1 << (2 * W)) * (1 << 24)
+    # no prime more than the bound needs: without the last one the product
+    # falls below 2^(2W + ceil(log2 n) + 3)
+    need = 2 * W + math.ceil(math.log2(n)) + 3 if n > 1 else 2 * W + 3
+    assert sum(math.log2(p) for p in ps[:-1]) < need <= sum(math.log2(p) for p in ps)
 
 
 def test_rns_primes_counts(lib):
-    """the headline 2048-bit n = 1024 product needs 264 primes (4 n 2^4096 <
-    M), i.e. 1056 int8 n^3 GEMMs, against the MFFT's 6 x 6144"""
+    """the headline 2048-bit n = 1024 product needs 258 primes (4 n 2^4096 <
+    M), i.e. 1032 int8 n^3 GEMMs, against the MFFT's 6 x 6144"""
     import mfft_ctypes
-    assert len(mfft_ctypes.rns_primes(1024, 128)) == 264
-    assert len(mfft_ctypes.rns_primes(256, 512)) % 8 == 0
+    assert len(mfft_ctypes.rns_primes(1024, 128)) == 258
 
 
 def test_rns_limits(lib):
