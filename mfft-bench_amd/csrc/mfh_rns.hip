@@ -116,12 +116,49 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
                                                      const RnsMod *__restrict__ mods, int nm,
                                                      uint16_t *__restrict__ R)
 {
+    constexpr int NE = 64 * EB;                  // elements of the workgroup
+    constexpr int RS = NE + 4;                   // LDS row stride (u16): the 4 lane
+                                                 // groups' rows fall in distinct banks
+    __shared__ __align__(16) uint16_t stg[2][32][RS];
+    // per wave: the digit pairs of 8 primes x 16 EB elements, rows padded so
+    // that the four lane groups' writes fall in distinct banks
+    __shared__ __align__(16) uint16_t tr[4][8][16 * EB + 8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int r = blockIdx.y;
-    const int k0 = (blockIdx.x * 4 + wave) * 16 * EB;
-    if (k0 >= np_) return;
+    const int kw0 = blockIdx.x * NE;             // first element of the workgroup
+    const int k0 = kw0 + wave * 16 * EB;         // first element of this wave
     const size_t nn = (size_t)n * n, npp = (size_t)np_ * np_;
+    // The limbs reach the registers through LDS, 32 limb planes at a time:
+    // 16-byte loads of 8 consecutive elements of one plane (coalesced; NE/64
+    // per thread and chunk), the next chunk's loads in flight while this
+    // chunk's fragments are read (two LDS buffers).  Limbs at or past L,
+    // rows at or past n and elements at or past n read as zero.
+    const bool vec = (n & 7) == 0 && ((uintptr_t)X & 15) == 0;   // 16-byte aligned rows
+    uint2 pre[EB][2];
+    auto load_chunk = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < EB; ++i) {
+            const int idx = threadIdx.x + 256 * i;
+            const int pl = idx / (NE / 8), g8 = idx % (NE / 8);
+            const int u = 32 * kb + pl, k = kw0 + 8 * g8;
+            uint4 v = uint4{0, 0, 0, 0};
+            if (r < n && u < L) {
+                const uint16_t *src = X + (size_t)u * nn + (size_t)r * n + k;
+                if (vec && k + 8 <= n) {
+                    v = *(const uint4 *)src;
+                } else {
+                    uint32_t w[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) w[j] = k + j < n ? src[j] : 0;
+                    v = uint4{w[0] | w[1] << 16, w[2] | w[3] << 16, w[4] | w[5] << 16,
+                              w[6] | w[7] << 16};
+                }
+            }
+            pre[i][0] = uint2{v.x, v.y};
+            pre[i][1] = uint2{v.z, v.w};
+        }
+    };
     v4i ef[KB][EB];
     int sb[EB];
     bool ok[EB];
@@ -129,26 +166,36 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
     for (int cb = 0; cb < EB; ++cb) {
         const int k = k0 + 16 * cb + col;
         ok[cb] = r < n && k < n;
-        const uint16_t *base = X + (ok[cb] ? (size_t)r * n + k : 0);
+        sb[cb] = 0;
+    }
+    load_chunk(0);
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
+        uint16_t (*buf)[RS] = stg[kb & 1];
+#pragma unroll
+        for (int i = 0; i < EB; ++i) {
+            const int idx = threadIdx.x + 256 * i;
+            const int pl = idx / (NE / 8), g8 = idx % (NE / 8);
+            *(uint2 *)&buf[pl][8 * g8] = pre[i][0];
+            *(uint2 *)&buf[pl][8 * g8 + 4] = pre[i][1];
+        }
+        __syncthreads();
+        if (kb + 1 < KB) load_chunk(kb + 1);
+#pragma unroll
+        for (int cb = 0; cb < EB; ++cb) {
+            const int e = wave * 16 * EB + 16 * cb + col;
             uint32_t d[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                // unconditional loads (limb index clamped, the value selected
-                // after): conditional ones each became a branch with a wait
-                const int u = 32 * kb + 8 * grp + 2 * q;
-                const uint32_t v0 = base[(size_t)min(u, L - 1) * nn];
-                const uint32_t v1 = base[(size_t)min(u + 1, L - 1) * nn];
-                const uint32_t x0 = (ok[cb] && u < L) ? v0 : 0;
-                const uint32_t x1 = (ok[cb] && u + 1 < L) ? v1 : 0;
-                d[q] = (x0 | (x1 << 16)) ^ 0x80808080u;      // bytes b - 128
+                const int u = 8 * grp + 2 * q;
+                d[q] = ((uint32_t)buf[u][e] | ((uint32_t)buf[u + 1][e] << 16)) ^ 0x80808080u;
             }
             ef[kb][cb] = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+            // the sign of a two's complement entry: bit 15 of limb L-1
+            if (sgn && kb == (L - 1) / 32) sb[cb] = ok[cb] ? buf[(L - 1) % 32][e] >> 15 : 0;
         }
-        const int top = base[(size_t)(L - 1) * nn] >> 15;
-        sb[cb] = (sgn && ok[cb]) ? top : 0;
     }
+    if (k0 >= np_) return;                       // past the padded row (after the barriers)
     // the weight fragments of output block ob + 1 are loaded while block ob
     // is multiplied (up to 8 k blocks; beyond that the registers hold the
     // element fragments)
@@ -179,22 +226,26 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm) {
             const int m = 8 * ob + 2 * grp + mm;
-            if (m >= nm) continue;               // zero weights past the last prime
-            const RnsMod md = mods[m];
-            uint16_t *dst = R + (size_t)m * npp + (size_t)r * np_;
+            const RnsMod md = mods[m < nm ? m : 0];
 #pragma unroll
             for (int cb = 0; cb < EB; ++cb) {
-                const int k = k0 + 16 * cb + col;
-                if (k >= np_) continue;
                 uint16_t w = 0;
-                if (ok[cb]) {
+                if (ok[cb] && m < nm) {
                     const int off = scaled ? (sb[cb] ? md.k1b : md.k0b) : (sb[cb] ? md.k1 : md.k0);
                     const double v = (double)acc[cb][2 * mm + 1] * 256.0 +
                                      (double)acc[cb][2 * mm] + (double)off;
                     w = rns_pair(rns_reduce(v, md.p, md.invp));
                 }
-                dst[k] = w;
+                tr[wave][2 * grp + mm][16 * cb + col] = w;
             }
+        }
+        // the wave's 16 EB consecutive elements of 8 primes, 16 bytes per
+        // lane: each store writes whole lines of the planes
+        if (lane < 16 * EB) {
+            const int pm = lane / (2 * EB), ch = lane % (2 * EB);
+            const int m = 8 * ob + pm;
+            const uint4 v = *(const uint4 *)&tr[wave][pm][8 * ch];
+            if (m < nm) *(uint4 *)(R + (size_t)m * npp + (size_t)r * np_ + k0 + 8 * ch) = v;
         }
     }
 }
