@@ -372,7 +372,10 @@ __global__ __launch_bounds__(64 * 2 * (8 / AB)) void k_rns_pointwise(
     TileMap tm, int R)
 {
     constexpr int NW = 2 * (8 / AB);
-    __shared__ PwStage s0, s1, s2, s3;
+    __shared__ PwStage s0, s1, s2;
+    // per wave: its 32 x 64 digit pairs of the finished tile, rows padded so
+    // that the four lane groups' writes fall in distinct banks
+    __shared__ __align__(16) uint16_t ytr[NW][16 * AB][72];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wi = wave >> 1, wj = wave & 1;
     const int T = tm.tpr * tm.tpr, nkb = np_ / 64;
@@ -434,40 +437,43 @@ __global__ __launch_bounds__(64 * 2 * (8 / AB)) void k_rns_pointwise(
         decode(c_it, m, ti, tj);
         c_it += wx;
         const RnsMod md = mods[m];
-        uint16_t *y = Y + m * npp;
 #pragma unroll
         for (int a = 0; a < AB; ++a)
 #pragma unroll
             for (int b = 0; b < 4; ++b)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const int i = ti * 128 + 16 * AB * wi + 16 * a + 4 * (lane >> 4) + v;
-                    const int j = tj * 128 + 64 * wj + 16 * b + (lane & 15);
                     const double cv = (double)acc.hh[a][b][v] * 65536.0 +
                                       (double)acc.md[a][b][v] * 256.0 + (double)acc.ll[a][b][v];
                     // B's residues carry the factor cinv: this is y_m
-                    y[(size_t)i * np_ + j] = rns_pair(rns_reduce(cv, md.p, md.invp));
+                    ytr[wave][16 * a + 4 * (lane >> 4) + v][16 * b + (lane & 15)] =
+                        rns_pair(rns_reduce(cv, md.p, md.invp));
                 }
+        // 16 bytes per lane: each store writes whole 128-byte rows of Y
+        uint16_t *y = Y + m * npp + (size_t)(ti * 128 + 16 * AB * wi) * np_ + tj * 128 + 64 * wj;
+#pragma unroll
+        for (int c = 0; c < 2 * AB; ++c) {
+            const int row = 8 * c + (lane >> 3), ch = lane & 7;
+            *(uint4 *)(y + (size_t)row * np_ + 8 * ch) = *(const uint4 *)&ytr[wave][row][8 * ch];
+        }
         zero();
     };
     zero();
-    // Four stages, three blocks in flight (with two, each block waited
-    // for copies issued only about 1000 MFMA cycles earlier).  Every step
-    // issues exactly 32 / NW copies per wave (past the last step it copies
-    // the last block again, into the stage just retired), so the
-    // outstanding copies are the same on every path: the compiler's own
-    // waits then stay at vmcnt(64 / NW) (with a conditional issue it waited
-    // for all copies, the ones just issued included, before every block).
-    // Stage g % 4 is complete once this wave's copies of g are (only those
-    // of g + 1 and g + 2 may be outstanding after them) and every wave has
-    // passed the barrier; the barrier also retires every read of stage
-    // (g + 3) % 4 (step g - 1), which the copies of g + 3 then overwrite.
+    // Three stages, two blocks in flight (a fourth stage measured no
+    // faster).  Every step issues exactly 32 / NW copies per wave (past the
+    // last step it copies the last block again, into the stage just
+    // retired), so the outstanding copies are the same on every path: the
+    // compiler's own waits then stay at vmcnt(32 / NW) (with a conditional
+    // issue it waited for all copies, the ones just issued included, before
+    // every block).  Stage g % 3 is complete once this wave's copies of g
+    // are (only those of g + 1 may be outstanding after them) and every wave
+    // has passed the barrier; the barrier also retires every read of stage
+    // (g + 2) % 3 (step g - 1), which the copies of g + 2 then overwrite.
     issue(s0);
     issue(s1);
-    issue(s2);
 #define RNS_STEP(S, SN, GG)                                                    \
     {                                                                          \
-        wait_vm_lgkm<64 / NW>();                                               \
+        wait_vm_lgkm<32 / NW>();                                               \
         __builtin_amdgcn_s_barrier();                                          \
         issue(SN);                                                             \
         rns_compute<AB>(S, wi, wj, lane, acc);                                 \
@@ -480,15 +486,13 @@ __global__ __launch_bounds__(64 * 2 * (8 / AB)) void k_rns_pointwise(
     // copied at every exit and spilled
     int g = 0;
 #pragma unroll 1
-    for (; g + 4 <= G; g += 4) {
-        RNS_STEP(s0, s3, g)
+    for (; g + 3 <= G; g += 3) {
+        RNS_STEP(s0, s2, g)
         RNS_STEP(s1, s0, g + 1)
         RNS_STEP(s2, s1, g + 2)
-        RNS_STEP(s3, s2, g + 3)
     }
-    if (g < G) RNS_STEP(s0, s3, g)
+    if (g < G) RNS_STEP(s0, s2, g)
     if (g + 1 < G) RNS_STEP(s1, s0, g + 1)
-    if (g + 2 < G) RNS_STEP(s2, s1, g + 2)
 #undef RNS_STEP
 }
 
@@ -956,6 +960,8 @@ int run_crt(const mfh_rns *r, uint16_t *out, int RL, int RLc)
     const bool narrow = nch <= 4, one = KBc <= 9;
     switch (r->crt_eb) {
     case 4:
+        // a batch sized to the k blocks: fewer registers, more workgroups
+        if (narrow && KBc <= 4) return launch_crt<4, 256, 4, false>(r, out, RL, RLc);
         if (narrow) return one ? launch_crt<4, 256, 9, false>(r, out, RL, RLc)
                                : launch_crt<4, 256, 4, true>(r, out, RL, RLc);
         return one ? launch_crt<4, 512, 9, false>(r, out, RL, RLc)
