@@ -13,6 +13,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "mfft_hip.h"
 #include "mfftbench.h"
 
 _Static_assert(sizeof(fpx_ctx) == 72, "fpx_ctx: 7 ints, 3 pointers, 2 doubles");
@@ -71,6 +72,33 @@ int r2_mm_mfft(int n, int L, uint64_t seed_a, uint64_t seed_b, int is_signed, in
         if (is_signed) mm_mfft_signed(A, B, n, L, &p, KERNEL_HIP, out, RL);
         else mm_mfft(A, B, n, L, &p, KERNEL_HIP, out, RL);
         rc = mfft_last_error();
+        if (!rc) rc = bigres_equal(out, want, n, RL, &bad[0], &bad[1], &bad[2]);
+    }
+    free(A); free(B); free(out);
+    return rc;
+}
+
+/* The multi-modular product (mfh_rns_*, include/mfft_hip.h; no reference
+ * counterpart) from C on the same seeded inputs: create, one host-buffer
+ * product, destroy, then bigres_equal against the expected limbs.  Returns 1
+ * when equal, 0 with bad = the first mismatch, or a negative error code
+ * (-100: allocation failure). */
+int r2_rns_mm(int n, int L, uint64_t seed_a, uint64_t seed_b, int is_signed,
+              const uint16_t *want, int RL, int *bad)
+{
+    uint16_t *A = bigmat_alloc(n, L), *B = bigmat_alloc(n, L);
+    uint16_t *out = malloc((size_t)RL * n * n * sizeof(uint16_t));
+    int rc = -100;
+    if (A && B && out) {
+        bigmat_rand(A, n, L, seed_a);
+        bigmat_rand(B, n, L, seed_b);
+        memset(out, 0xA5, (size_t)RL * n * n * sizeof(uint16_t));
+        mfh_rns *r = NULL;
+        rc = mfh_rns_create(&r, n, L);
+        if (!rc) {
+            rc = mfh_rns_mm(r, is_signed ? MFH_IN_U16_SIGNED : MFH_IN_U16, A, B, out, RL);
+            mfh_rns_destroy(r);
+        }
         if (!rc) rc = bigres_equal(out, want, n, RL, &bad[0], &bad[1], &bad[2]);
     }
     free(A); free(B); free(out);

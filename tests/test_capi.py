@@ -44,6 +44,7 @@ def r2(lib):
     d.r2_instrumentation.argtypes = [i, i, vp, vp]
     d.r2_fpx_f32.argtypes = [vp, vp, i, i, vp, vp, vp]
     d.r2_fpx_f64.argtypes = [vp, vp, i, i, vp, vp, vp, vp]
+    d.r2_rns_mm.argtypes = [i, i, u64, u64, i, vp, i, vp]
     return d
 
 
@@ -141,6 +142,23 @@ def test_route2_mm_mfft_products(gpu, r2, rec):
         assert rc == 1, (rc, bad.tolist())
         ran += 1
     assert ran >= len(cases) - 2
+
+
+@pytest.mark.gpu
+def test_route2_rns_products(gpu, r2):
+    """the multi-modular product called from C (mfh_rns_create / mfh_rns_mm /
+    mfh_rns_destroy) on the seeded inputs of every golden product, unsigned
+    and two's complement, checked by bigres_equal in C"""
+    with open(os.path.join(GOLD, "products.json")) as f:
+        cases = json.load(f)
+    for c in cases:
+        n, L, RL = c["n"], c["L"], c["RL"]
+        print(f"[route2 rns] n={n} L={L} signed={c['signed']}", flush=True)
+        want = np.array(c["out"], dtype=np.uint16)
+        bad = np.zeros(3, np.int32)
+        rc = r2.r2_rns_mm(n, L, c["seed_a"], c["seed_b"], int(c["signed"]), want.ctypes.data,
+                          RL, bad.ctypes.data)
+        assert rc == 1, (n, L, c["signed"], rc, bad.tolist())
 
 
 @pytest.mark.gpu
