@@ -192,22 +192,33 @@ def cpu_baseline(n, L, nprod_total):
                         f"mm_mfft at n={ns} ({rest_small:.3f} s) x {scale:.0f}; extrapolated"))
 
 
-def rns_measure(n, L, kind, dA, dB, steps, warmup, want=None):
+def rns_measure(n, L, kind, dA, dB, steps, warmup, want=None, fpx_scale=None):
     """The multi-modular product (mfh_rns_*) of the same device-resident
     inputs: ms per product, stage times, the int8 GEMMs it issues, and
-    whether its limbs equal `want` (the MFFT product's)."""
+    whether its output equals `want` (the MFFT product's).  With
+    fpx_scale = (SA, SB) the inputs are fp32 on an L-limb grid and the
+    product is mfh_rns_fpx_mm_dev's (encode, L + 1 two's complement limbs
+    multiplied, decode); the stage times cover its integer product."""
     import numpy as np
     import mfft_ctypes as M
+    fp32 = fpx_scale is not None
+    Lr = L + 1 if fp32 else L
     RL = 2 * L + 1
     lib = M.load()
     try:
-        r = M.Rns(n, L)
+        r = M.Rns(n, Lr)
     except M.MfftError as e:
-        log(f"[bench] multi-modular n={n} L={L}: {e}")
+        log(f"[bench] multi-modular n={n} L={Lr}: {e}")
         return None
-    dO = M.DevBuf(RL * n * n * 2)
-    step = lambda: M.check(lib.mfh_rns_mm_dev(r.h, kind, dA.ptr, dB.ptr, dO.ptr, RL),
-                           "mfh_rns_mm_dev")
+    if fp32:
+        SA, SB = fpx_scale
+        dO = M.DevBuf(n * n * 4)
+        step = lambda: M.check(lib.mfh_rns_fpx_mm_dev(r.h, dA.ptr, dB.ptr, SA, SB, dO.ptr),
+                               "mfh_rns_fpx_mm_dev")
+    else:
+        dO = M.DevBuf(RL * n * n * 2)
+        step = lambda: M.check(lib.mfh_rns_mm_dev(r.h, kind, dA.ptr, dB.ptr, dO.ptr, RL),
+                               "mfh_rns_mm_dev")
     for _ in range(max(1, warmup)):
         step()
     r.sync()
@@ -225,7 +236,8 @@ def rns_measure(n, L, kind, dA, dB, steps, warmup, want=None):
     res_ops, pw_ops, crt_ops = r.work()
     equal = None
     if want is not None:
-        equal = bool(np.array_equal(dO.download(np.uint16, RL * n * n), want))
+        got = dO.download(np.uint32, n * n) if fp32 else dO.download(np.uint16, RL * n * n)
+        equal = bool(np.array_equal(got, want))
     dO.free()
     r.close()
     log(f"[bench] multi-modular: {ms:.3f} ms/product, stages(ms) residues {st[0]:.3f} "
@@ -237,9 +249,13 @@ def rns_measure(n, L, kind, dA, dB, steps, warmup, want=None):
             "int8_ops": {"residues": res_ops, "per_prime_gemms": pw_ops, "crt": crt_ops},
             "per_prime_gemm_tops": round(pw_ops / (st[1] * 1e-3) / 1e12, 1),
             "device_bytes": nbytes, "equal_to_mfft": equal,
-            "note": ("exact product by residues mod 16-bit primes (mfh_rns_mm_dev), same "
-                     "inputs and output limbs as the MFFT product; no counterpart in the "
-                     "reference")}
+            "note": (("fp32 product on the same grid by residues mod 16-bit primes "
+                      "(mfh_rns_fpx_mm_dev: encode to L+1 two's complement limbs, exact "
+                      "product, decode), same inputs and output bits as the MFFT path"
+                      if fp32 else
+                      "exact product by residues mod 16-bit primes (mfh_rns_mm_dev), same "
+                      "inputs and output limbs as the MFFT product") +
+                     "; no counterpart in the reference")}
 
 
 def method_table(args):
@@ -536,9 +552,13 @@ def main():
         pass
 
     mm = None
-    if not fp32 and not args.no_rns:
-        mfft_out = dO.download(np.uint16, RL * n * n)
-        mm = rns_measure(n, L, kind, dA, dB, args.steps, args.warmup, mfft_out)
+    if not args.no_rns:
+        if fp32:
+            mm = rns_measure(n, L, kind, dA, dB, args.steps, args.warmup,
+                             dO.download(np.uint32, n * n), fpx_scale=(SA, SB))
+        else:
+            mm = rns_measure(n, L, kind, dA, dB, args.steps, args.warmup,
+                             dO.download(np.uint16, RL * n * n))
 
     cpu = None
     if not args.no_cpu_baseline:

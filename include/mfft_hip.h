@@ -267,6 +267,21 @@ int  mfh_rns_mm(mfh_rns *ctx, int in_kind, const uint16_t *A, const uint16_t *B,
  * lo | hi << 8 (r mod p = 256 (int8)hi + (int8)lo, |r| <= (p-1)/2), zero
  * outside n x n (a stage of mfh_rns_mm_dev, for tests) */
 int  mfh_rns_residues_dev(mfh_rns *ctx, int in_kind, const void *dX, void *dR);
+/* The fixed-point products of mfh_fpx_mm / mfh_fpx_mm_f64 (fpx_encode,
+ * fpx_mm_f32, fpx_decode: src/fpfixed.c:144-322) by the multi-modular
+ * product: on a grid of L limbs the context is created with L + 1 limbs
+ * (mfh_rns_create(&ctx, n, L + 1); the limb above the grid carries the sign
+ * of the two's complement operands).  Same inputs, scales and single
+ * rounding as mfh_fpx_mm_dev on an L-limb context, so the same outputs bit
+ * for bit.  The first call allocates the encoded operands and product
+ * limbs ((4 L + 4) n^2 bytes, kept with the context). */
+int  mfh_rns_fpx_mm_dev(mfh_rns *ctx, const void *dA, const void *dB, int SA, int SB,
+                        void *dC);
+int  mfh_rns_fpx_mm_f64_dev(mfh_rns *ctx, const void *dA, const void *dB, int SA, int SB,
+                            void *dC);
+int  mfh_rns_fpx_mm(mfh_rns *ctx, const float *A, const float *B, int SA, int SB, float *C);
+int  mfh_rns_fpx_mm_f64(mfh_rns *ctx, const double *A, const double *B, int SA, int SB,
+                        double *C);
 int  mfh_rns_sync(mfh_rns *ctx);
 /* stage times of the most recent product while timing is on: [0] B
  * transposed and the residues of both operands, [1] the per-prime GEMMs,

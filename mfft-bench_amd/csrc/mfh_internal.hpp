@@ -206,6 +206,15 @@ int mfh_launch_carry_planes(const int64_t *Cw, int P, size_t nn, uint16_t *out,
 // fp32 (is_f64 = 0) or fp64 matrix -> L signed limb planes at scale 2^S
 int mfh_launch_encode(const void *X, int is_f64, int n, int L, int S, int32_t *out,
                       hipStream_t st);
+// fp32 (is_f64 = 0) or fp64 matrix -> the L + 1 two's complement uint16 limb
+// planes of the value mfh_launch_encode puts on an L-limb grid (the
+// multi-modular product's input form)
+int mfh_launch_encode_tc(const void *X, int is_f64, int n, int L, int S, uint16_t *out,
+                         hipStream_t st);
+// RLr carried two's complement limb planes -> floats at scale 2^-SAB, the
+// decode of the coefficient planes of the same value (fmt: MFH_DEC_F32/F64)
+int mfh_launch_decode_limbs(const uint16_t *limbs, size_t nn, int RLr, int SAB, int fmt,
+                            void *out, int32_t *out2, hipStream_t st);
 // 2L-1 coefficient planes -> floats at scale 2^-SAB (fmt: MFH_DEC_*)
 int mfh_launch_decode(mfh_ctx *c, const int64_t *Cw, int SAB, int fmt, void *out,
                       int32_t *out2);

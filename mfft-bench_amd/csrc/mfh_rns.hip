@@ -795,6 +795,7 @@ struct mfh_rns {
     v4i *dW, *dWb, *dT;
     int8_t *dMb;
     uint16_t *dRA, *dRB, *dY, *dBt;
+    uint16_t *dFA, *dFB, *dFO;  // fixed-point products: operand and product limbs
     size_t bytes;
     int timing;
     hipEvent_t ev[4];
@@ -1045,7 +1046,8 @@ void mfh_rns_destroy(mfh_rns *r)
 {
     if (!r) return;
     if (r->stream) (void)hipStreamSynchronize(r->stream);
-    void *bufs[] = {r->dMod, r->dW, r->dWb, r->dT, r->dMb, r->dRA, r->dRB, r->dY, r->dBt};
+    void *bufs[] = {r->dMod, r->dW, r->dWb, r->dT, r->dMb, r->dRA, r->dRB, r->dY, r->dBt,
+                    r->dFA,  r->dFB, r->dFO};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     for (auto &e : r->ev)
@@ -1119,6 +1121,80 @@ int mfh_rns_mm(mfh_rns *r, int in_kind, const uint16_t *A, const uint16_t *B, ui
     for (void *p : {dA, dB, dO})
         if (p) (void)hipFree(p);
     return rc;
+}
+
+}  // extern "C"
+
+namespace {
+// fp32 (f64 = 0) or fp64 matrices on the fixed-point grid of L - 1 limbs (L
+// the context's): both encoded as the L two's complement limbs of their grid
+// values, multiplied exactly (2L limbs hold n 2^(32 (L-1)) with its sign),
+// and decoded with the single rounding of the grid's decode
+// (src/fpfixed.c:144-204, 212-322)
+int rns_fpx(mfh_rns *r, int f64, const void *dA, const void *dB, int SA, int SB, void *dC)
+{
+    if (!r || !dA || !dB || !dC) return MFH_E_ARG;
+    if (r->L < 2) return MFH_E_ARG;
+    const int Lg = r->L - 1, RLr = 2 * r->L;
+    const size_t nn = (size_t)r->n * r->n;
+    int rc = MFH_OK;
+    if (!r->dFO) {
+        rc = rns_alloc(r, (void **)&r->dFA, (size_t)r->L * nn * 2);
+        if (!rc) rc = rns_alloc(r, (void **)&r->dFB, (size_t)r->L * nn * 2);
+        if (!rc) rc = rns_alloc(r, (void **)&r->dFO, (size_t)RLr * nn * 2);
+        if (rc) return rc;
+    }
+    if ((rc = mfh_launch_encode_tc(dA, f64, r->n, Lg, SA, r->dFA, r->stream))) return rc;
+    if ((rc = mfh_launch_encode_tc(dB, f64, r->n, Lg, SB, r->dFB, r->stream))) return rc;
+    if ((rc = mfh_rns_mm_dev(r, MFH_IN_U16_SIGNED, r->dFA, r->dFB, r->dFO, RLr))) return rc;
+    return mfh_launch_decode_limbs(r->dFO, nn, RLr, SA + SB, f64 ? MFH_DEC_F64 : MFH_DEC_F32,
+                                   dC, nullptr, r->stream);
+}
+
+int rns_fpx_host(mfh_rns *r, int f64, const void *A, const void *B, int SA, int SB, void *C)
+{
+    if (!r || !A || !B || !C) return MFH_E_ARG;
+    const size_t bytes = (size_t)r->n * r->n * (f64 ? 8 : 4);
+    void *dA = nullptr, *dB = nullptr, *dC = nullptr;
+    int rc = MFH_OK;
+    if (hipMalloc(&dA, bytes) != hipSuccess || hipMalloc(&dB, bytes) != hipSuccess ||
+        hipMalloc(&dC, bytes) != hipSuccess)
+        rc = MFH_E_NOMEM;
+    if (!rc && (hipMemcpyAsync(dA, A, bytes, hipMemcpyHostToDevice, r->stream) != hipSuccess ||
+                hipMemcpyAsync(dB, B, bytes, hipMemcpyHostToDevice, r->stream) != hipSuccess))
+        rc = MFH_E_HIP;
+    if (!rc) rc = rns_fpx(r, f64, dA, dB, SA, SB, dC);
+    if (!rc && hipMemcpyAsync(C, dC, bytes, hipMemcpyDeviceToHost, r->stream) != hipSuccess)
+        rc = MFH_E_HIP;
+    if (hipStreamSynchronize(r->stream) != hipSuccess && !rc) rc = MFH_E_HIP;
+    for (void *p : {dA, dB, dC})
+        if (p) (void)hipFree(p);
+    return rc;
+}
+}  // namespace
+
+extern "C" {
+
+int mfh_rns_fpx_mm_dev(mfh_rns *r, const void *dA, const void *dB, int SA, int SB, void *dC)
+{
+    return rns_fpx(r, 0, dA, dB, SA, SB, dC);
+}
+
+int mfh_rns_fpx_mm_f64_dev(mfh_rns *r, const void *dA, const void *dB, int SA, int SB,
+                           void *dC)
+{
+    return rns_fpx(r, 1, dA, dB, SA, SB, dC);
+}
+
+int mfh_rns_fpx_mm(mfh_rns *r, const float *A, const float *B, int SA, int SB, float *C)
+{
+    return rns_fpx_host(r, 0, A, B, SA, SB, C);
+}
+
+int mfh_rns_fpx_mm_f64(mfh_rns *r, const double *A, const double *B, int SA, int SB,
+                       double *C)
+{
+    return rns_fpx_host(r, 1, A, B, SA, SB, C);
 }
 
 int mfh_rns_sync(mfh_rns *r)

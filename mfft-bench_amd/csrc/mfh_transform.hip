@@ -1216,6 +1216,49 @@ __global__ __launch_bounds__(256) void k_encode(Src src, int32_t *__restrict__ o
     }
 }
 
+// fp32 / fp64 entries -> the two's complement uint16 limbs of the value
+// k_encode puts on the grid (its limbs below src.L, i.e. x 2^S truncated to
+// the grid) over src.L + 1 limbs: |value| < 2^(16 L), so the top limb holds
+// the sign.  This is the multi-modular product's input form.
+template <class Src>
+__global__ __launch_bounds__(256) void k_encode_tc(Src src, uint16_t *__restrict__ out)
+{
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= src.nn) return;
+    const int i = (int)(e / src.n), k = (int)(e % src.n);
+    int lo, r[Src::NW];
+    src.window(i, k, lo, r);
+    int carry = 0;
+    for (int u = 0; u <= src.L; ++u) {
+        int v = carry;
+        if (u < src.L) {
+#pragma unroll
+            for (int t = 0; t < Src::NW; ++t) v += u == lo + t ? r[t] : 0;
+        }
+        out[(size_t)u * src.nn + e] = (uint16_t)(v & 0xFFFF);
+        carry = v >> 16;
+    }
+}
+
+// The fixed-point decode (decode_value) from RLr carried two's complement
+// limbs: limb w as a plane, the top one sign-extended.  The decode carries
+// them again (a no-op) over one more limb, so the window and the rounding
+// are those of the coefficient-plane decode of the same value.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_decode_limbs(const uint16_t *__restrict__ limbs,
+                                                      size_t nn, int RLr, int SAB,
+                                                      void *__restrict__ out, int32_t *out2)
+{
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= nn) return;
+    decode_value<FMT>(
+        [&](int w) -> int64_t {
+            const uint16_t x = limbs[(size_t)w * nn + e];
+            return w == RLr - 1 ? (int64_t)(int16_t)x : (int64_t)x;
+        },
+        RLr, RLr + 1, SAB, out, out2, e);
+}
+
 // ---- plane transpose (B operand) -----------------------------------------------
 // uint16 planes with n a multiple of 64 (whole 64 x 64 tiles): 16-byte
 // loads of 8 consecutive elements of a row, 16-byte stores of 8 consecutive
@@ -1643,6 +1686,37 @@ int mfh_launch_encode(const void *X, int is_f64, int n, int L, int S, int32_t *o
     else
         hipLaunchKernelGGL(k_encode<SrcF32>, grid, dim3(256), 0, st,
                            SrcF32{(const float *)X, nn, n, L, S}, out);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_encode_tc(const void *X, int is_f64, int n, int L, int S, uint16_t *out,
+                         hipStream_t st)
+{
+    const size_t nn = (size_t)n * n;
+    const dim3 grid((unsigned)((nn + 255) / 256));
+    if (is_f64)
+        hipLaunchKernelGGL(k_encode_tc<SrcF64>, grid, dim3(256), 0, st,
+                           SrcF64{(const double *)X, nn, n, L, S}, out);
+    else
+        hipLaunchKernelGGL(k_encode_tc<SrcF32>, grid, dim3(256), 0, st,
+                           SrcF32{(const float *)X, nn, n, L, S}, out);
+    MFH_HIP(hipGetLastError());
+    return MFH_OK;
+}
+
+int mfh_launch_decode_limbs(const uint16_t *limbs, size_t nn, int RLr, int SAB, int fmt,
+                            void *out, int32_t *out2, hipStream_t st)
+{
+    const dim3 grid((unsigned)((nn + 255) / 256));
+    if (fmt == MFH_DEC_F32)
+        hipLaunchKernelGGL(k_decode_limbs<MFH_DEC_F32>, grid, dim3(256), 0, st, limbs, nn, RLr,
+                           SAB, out, out2);
+    else if (fmt == MFH_DEC_F64)
+        hipLaunchKernelGGL(k_decode_limbs<MFH_DEC_F64>, grid, dim3(256), 0, st, limbs, nn, RLr,
+                           SAB, out, out2);
+    else
+        return MFH_E_ARG;
     MFH_HIP(hipGetLastError());
     return MFH_OK;
 }

@@ -146,6 +146,10 @@ def load(path=None):
         "mfh_rns_mm_dev": ([vp, i, vp, vp, vp, i], i),
         "mfh_rns_mm": ([vp, i, vp, vp, vp, i], i),
         "mfh_rns_residues_dev": ([vp, i, vp, vp], i),
+        "mfh_rns_fpx_mm_dev": ([vp, vp, vp, i, i, vp], i),
+        "mfh_rns_fpx_mm_f64_dev": ([vp, vp, vp, i, i, vp], i),
+        "mfh_rns_fpx_mm": ([vp, vp, vp, i, i, vp], i),
+        "mfh_rns_fpx_mm_f64": ([vp, vp, vp, i, i, vp], i),
         "mfh_rns_sync": ([vp], i), "mfh_rns_set_timing": ([vp, i], i),
         "mfh_rns_stage_times": ([vp, C.POINTER(C.c_float)], i),
         "mfh_rns_work": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_double),
@@ -335,6 +339,22 @@ class Rns:
     def mm_dev(self, dA, dB, dOut, RL, signed=False):
         kind = MFH_IN_U16_SIGNED if signed else MFH_IN_U16
         check(self.lib.mfh_rns_mm_dev(self.h, kind, dA, dB, dOut, RL), "mfh_rns_mm_dev")
+
+    def fpx_mm(self, A, B, SA, SB):
+        """fp32 product on the grid of L - 1 limbs (the context has L)"""
+        out = np.empty(self.n * self.n, dtype=np.float32)
+        check(self.lib.mfh_rns_fpx_mm(self.h, _p(A), _p(B), SA, SB, _p(out)), "mfh_rns_fpx_mm")
+        return out
+
+    def fpx_mm_f64(self, A, B, SA, SB):
+        out = np.empty(self.n * self.n, dtype=np.float64)
+        check(self.lib.mfh_rns_fpx_mm_f64(self.h, _p(A), _p(B), SA, SB, _p(out)),
+              "mfh_rns_fpx_mm_f64")
+        return out
+
+    def fpx_mm_dev(self, dA, dB, SA, SB, dC, f64=False):
+        fn = self.lib.mfh_rns_fpx_mm_f64_dev if f64 else self.lib.mfh_rns_fpx_mm_dev
+        check(fn(self.h, dA, dB, SA, SB, dC), "mfh_rns_fpx_mm_dev")
 
     def residues(self, X, signed=False):
         """digit-pair residues [primes][np][np] of one operand (rows r, inner k)"""
