@@ -403,6 +403,9 @@ def main():
     ap.add_argument("--no-verify", action="store_true")
     ap.add_argument("--no-rns", action="store_true",
                     help="skip the multi-modular product reported beside the MFFT one")
+    ap.add_argument("--rns-only", action="store_true",
+                    help="only the multi-modular product of the workload (--warmup untimed, "
+                         "--steps timed; no MFFT kernels run), e.g. for counter passes")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run the plain copy kernel over MIB MiB, --steps times (the "
                          "known-size kernel that HBM byte counters are calibrated against)")
@@ -480,9 +483,24 @@ def main():
     L = W // 16
     RL = 2 * L + 1
     lib = M.load()
+    SA = SB = W // 2
+    if args.rns_only:
+        eb = 4 * n * n if fp32 else L * n * n * 2
+        dA, dB = M.DevBuf(eb), M.DevBuf(eb)
+        for d, seed in ((dA, 12345), (dB, 12345 ^ 0xABCDEF)):
+            if fp32:
+                M.check(lib.mfh_rand_f32_dev(None, d.ptr, n * n, seed, -20, 20))
+            else:
+                M.check(lib.mfh_rand_u16_dev(None, d.ptr, n, L, seed))
+        M.check(lib.mfh_sync(None))
+        kind = M.MFH_IN_U16_SIGNED if signed else M.MFH_IN_U16
+        mm = rns_measure(n, L, kind, dA, dB, args.steps, args.warmup,
+                         fpx_scale=(SA, SB) if fp32 else None)
+        print(json.dumps({"workload": args.config, "n": n, "width_bits": W, "entries": ekind,
+                          "multimodular": mm}), flush=True)
+        return
     p = M.plan(L)
     ctx = M.Ctx(n, L, p)
-    SA = SB = W // 2
     if fp32:
         dA, dB, dO = M.DevBuf(n * n * 4), M.DevBuf(n * n * 4), M.DevBuf(n * n * 4)
         M.check(lib.mfh_rand_f32_dev(ctx.h, dA.ptr, n * n, 12345, -20, 20))
