@@ -551,22 +551,29 @@ TileMap tile_map(int tpr, int wx)
 // zero for m >= nm.
 // NT threads (512, or 256 for narrow outputs of at most four chunks);
 // KBB: the T fragments of a chunk are loaded in batches of KBB k blocks,
-// double-buffered (DBL), or all at once (KBB >= KBc, one wait per chunk)
-template <int EB, int NT, int KBB, bool DBL>
+// double-buffered (DBL), or all at once (KBB >= KBc, one wait per chunk).
+// Wide outputs run in nh passes over ranges of cpp = ceil(nch / nh) output
+// chunks, low to high: the LDS then holds one pass's int64 groups, which
+// leaves room for more elements per workgroup (each T fragment serves E
+// elements), and each pass carries into the next.  MP: compiled for more
+// than one pass (otherwise nh = 1 and the pass loop folds away, which keeps
+// the single-pass kernels' registers as they were).
+template <int EB, int NT, int KBB, bool DBL, bool MP>
 __global__ __launch_bounds__(NT) void k_rns_crt(
-    const uint16_t *__restrict__ Y, int n, int np_, int nm, int KBc, int Jpad,
+    const uint16_t *__restrict__ Y, int n, int np_, int nm, int KBc, int Jpad, int nh,
     const v4i *__restrict__ T, const int8_t *__restrict__ mb, const RnsMod *__restrict__ mods,
     uint16_t *__restrict__ out, int RL, int RLc)
 {
     constexpr int E = 16 * EB, SEGS = NT / E, NW = NT / 64;
+    const int nch = Jpad / 64, cpp = MP ? (nch + nh - 1) / nh : nch;
     extern __shared__ __align__(16) unsigned char smem[];
     v4i *yl = (v4i *)smem;                                        // KBc*EB*64
-    long long *grp = (long long *)(yl + (size_t)KBc * EB * 64);  // [G][E]
-    const int G = Jpad / 4;
-    long long *segc = grp + (size_t)G * E;                        // [SEGS][E] x 4
+    long long *grp = (long long *)(yl + (size_t)KBc * EB * 64);  // [16 cpp][E]
+    long long *segc = grp + (size_t)16 * cpp * E;                 // [SEGS][E] x 4
     long long *seglo = segc + NT, *seghi = seglo + NT, *segin = seghi + NT;
     double *qs = (double *)(segin + NT);                          // [NT]
     long long *qv = (long long *)(qs + NT);                       // [E]
+    long long *cin = qv + E;                                      // [E]: carry into the pass
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i = blockIdx.y, j0 = blockIdx.x * E;
@@ -605,16 +612,19 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
         double t = 0;
         for (int r = 0; r < SEGS; ++r) t += qs[r * E + tid];
         qv[tid] = (long long)rint(t);
+        if (MP) cin[tid] = 0;
     }
     __syncthreads();
 
+    // one pass: output chunks c0 .. c1-1, their groups G0 = 16 c0 .. Gb-1
+    // that hold output limbs
+    auto pass = [&](const int c0, const int c1, const int G0, const int Gb) {
     // 2. byte columns: GEMM over the y digits, q M subtracted, groups of 4.
     //    A wave takes chunks of 64 output bytes (4 fragment rows); the T
     //    fragments of a chunk stream in batches of KBB k blocks, the next
     //    batch loaded while the current one is multiplied (DBL), or arrive
     //    all at once.
-    const int nch = Jpad / 64;
-    for (int ch = wave; ch < nch; ch += NW) {
+    for (int ch = c0 + wave; ch < c1; ch += NW) {
         v4i acc[4][EB];
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj)
@@ -668,30 +678,32 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
 #pragma unroll
                 for (int v = 3; v >= 0; --v)
                     g = g * 256 + ((long long)acc[jj][cb][v] - q * (long long)mb[4 * gi + v]);
-                grp[(size_t)gi * E + el] = g;
+                grp[(size_t)(gi - G0) * E + el] = g;
             }
     }
     __syncthreads();
 
-    // 3. carry lookahead over the Gc groups that hold the RLc output limbs:
-    // SEGS runs of len >= 2 groups per element.  A run propagates with
-    // carry-in 0 (its 32-bit words Ls, carry-out c); with the true carry-in
-    // X (|X| < 2^40) its carry-out is c + 1 when X >= 2^(32 len) - Ls,
-    // c - 1 when X < -Ls, else c.  Ls's low 64 bits and whether its higher
-    // words are all 0 or all 1 give both thresholds whenever they are
-    // representable; otherwise the case cannot occur.  The last run's
-    // carry-out is discarded (it lies above the output).
+    // 3. carry lookahead over this pass's groups G0 .. Gb-1 (of the Gc that
+    // hold the RLc output limbs): SEGS runs of len >= 2 groups per element.
+    // A run propagates with carry-in 0 (its 32-bit words Ls, carry-out c);
+    // with the true carry-in X (|X| < 2^40) its carry-out is c + 1 when
+    // X >= 2^(32 len) - Ls, c - 1 when X < -Ls, else c.  Ls's low 64 bits
+    // and whether its higher words are all 0 or all 1 give both thresholds
+    // whenever they are representable; otherwise the case cannot occur.  The
+    // last run may be shorter and runs past it empty: their carry-outs are
+    // not used; the carry into the next pass is the last run's exact one,
+    // from its propagation with the true carry-in below.
     const int Gc = (RLc + 1) / 2;
-    int len = (Gc + SEGS - 1) / SEGS;
+    int len = (Gb - G0 + SEGS - 1) / SEGS;
     if (len < 2) len = 2;
     const int el = tid % E, sg = tid / E;
-    const int g0 = sg * len, g1 = min(g0 + len, Gc);
+    const int g0 = G0 + sg * len, g1 = min(g0 + len, Gb);
     {
         long long cc = 0;
         uint64_t low = 0;
         bool zero_hi = true, ones_hi = true;
         for (int g = g0; g < g1; ++g) {
-            const long long v = cc + grp[(size_t)g * E + el];
+            const long long v = cc + grp[(size_t)(g - G0) * E + el];
             const uint64_t w = (uint64_t)v & 0xFFFFFFFFull;
             const int ix = g - g0;
             if (ix < 2) low |= w << (32 * ix);
@@ -709,7 +721,7 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
     }
     __syncthreads();
     if (tid < E) {
-        long long C = 0;
+        long long C = MP ? cin[tid] : 0;
         for (int r = 0; r < SEGS; ++r) {
             segin[r * E + tid] = C;
             C = segc[r * E + tid] + (C >= seghi[r * E + tid]) - (C < seglo[r * E + tid]);
@@ -721,7 +733,7 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
         uint16_t *o = out + (size_t)i * n + j0 + el;
         uint32_t top = 0;
         for (int g = g0; g < g1; ++g) {
-            const long long v = cc + grp[(size_t)g * E + el];
+            const long long v = cc + grp[(size_t)(g - G0) * E + el];
             const uint32_t w = (uint32_t)v;
             const int u = 2 * g;
             o[(size_t)u * nn] = (uint16_t)w;
@@ -738,12 +750,31 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
             for (int u = RLc; u < RL; ++u) o[(size_t)u * nn] = ext;
         }
     }
+    // the exact carry into group Gb (the next pass's carry-in): the last
+    // non-empty run's, propagated above with its true carry-in (also for
+    // columns at or past n, which write nothing)
+    if (MP && g1 == Gb && g0 < g1) {
+        long long cc = segin[sg * E + el];
+        for (int g = g0; g < g1; ++g) cc = (cc + grp[(size_t)(g - G0) * E + el]) >> 32;
+        cin[el] = cc;
+    }
+    };
+    const int Gc = (RLc + 1) / 2;         // groups that hold the RLc output limbs
+    if constexpr (MP) {
+        for (int c0 = 0; c0 < nch && 16 * c0 < Gc; c0 += cpp) {
+            const int c1 = min(c0 + cpp, nch);
+            pass(c0, c1, 16 * c0, min(16 * c1, Gc));
+            __syncthreads();   // grp, the runs and cin are reused by the next pass
+        }
+    } else {
+        pass(0, nch, 0, Gc);
+    }
 }
 
-size_t crt_lds_bytes(int EB, int NT, int KBc, int Jpad)
+size_t crt_lds_bytes(int EB, int NT, int KBc, int Jpad, int nh)
 {
-    const int E = 16 * EB;
-    return (size_t)KBc * EB * 1024 + (size_t)(Jpad / 4) * E * 8 + 5 * NT * 8 + E * 8;
+    const int E = 16 * EB, cpp = (Jpad / 64 + nh - 1) / nh;
+    return (size_t)KBc * EB * 1024 + (size_t)16 * cpp * E * 8 + 5 * NT * 8 + 2 * E * 8;
 }
 
 // ---- host planning ---------------------------------------------------------
@@ -818,7 +849,7 @@ int kres_blocks(int L)
 }  // namespace
 
 struct mfh_rns {
-    int n, np, L, nm, nmk, KB, Jpad, crt_eb;
+    int n, np, L, nm, nmk, KB, Jpad, crt_eb, crt_nh;
     int cus;              // compute units (8 XCDs of cus / 8)
     int dev;
     hipStream_t stream;
@@ -965,20 +996,20 @@ int run_residue(const mfh_rns *r, const uint16_t *X, int sgn, int scaled, uint16
     return MFH_OK;
 }
 
-template <int EB, int NT, int KBB, bool DBL>
+template <int EB, int NT, int KBB, bool DBL, bool MP = false>
 int launch_crt(const mfh_rns *r, uint16_t *out, int RL, int RLc)
 {
     const int KBc = r->nmk / 32;
-    const size_t lds = crt_lds_bytes(EB, NT, KBc, r->Jpad);
+    const size_t lds = crt_lds_bytes(EB, NT, KBc, r->Jpad, r->crt_nh);
     static bool attr_set = false;
     if (!attr_set) {
-        MFH_HIP(hipFuncSetAttribute((const void *)k_rns_crt<EB, NT, KBB, DBL>,
+        MFH_HIP(hipFuncSetAttribute((const void *)k_rns_crt<EB, NT, KBB, DBL, MP>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         attr_set = true;
     }
     dim3 grid((r->n + 16 * EB - 1) / (16 * EB), r->n);
-    hipLaunchKernelGGL((k_rns_crt<EB, NT, KBB, DBL>), grid, dim3(NT), lds, r->stream, r->dY,
-                       r->n, r->np, r->nm, KBc, r->Jpad, (const v4i *)r->dT, r->dMb,
+    hipLaunchKernelGGL((k_rns_crt<EB, NT, KBB, DBL, MP>), grid, dim3(NT), lds, r->stream, r->dY,
+                       r->n, r->np, r->nm, KBc, r->Jpad, r->crt_nh, (const v4i *)r->dT, r->dMb,
                        (const RnsMod *)r->dMod, out, RL, RLc);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
@@ -989,19 +1020,25 @@ int launch_crt(const mfh_rns *r, uint16_t *out, int RL, int RLc)
 int run_crt(const mfh_rns *r, uint16_t *out, int RL, int RLc)
 {
     const int KBc = r->nmk / 32, nch = r->Jpad / 64;
-    const bool narrow = nch <= 4, one = KBc <= 9;
+    const bool narrow = nch <= 4 && r->crt_nh == 1, one = KBc <= 9, mp = r->crt_nh > 1;
     switch (r->crt_eb) {
     case 4:
         // a batch sized to the k blocks: fewer registers, more workgroups
         if (narrow && KBc <= 4) return launch_crt<4, 256, 4, false>(r, out, RL, RLc);
         if (narrow) return one ? launch_crt<4, 256, 9, false>(r, out, RL, RLc)
                                : launch_crt<4, 256, 4, true>(r, out, RL, RLc);
+        if (mp) return one ? launch_crt<4, 512, 9, false, true>(r, out, RL, RLc)
+                           : launch_crt<4, 512, 4, true, true>(r, out, RL, RLc);
         return one ? launch_crt<4, 512, 9, false>(r, out, RL, RLc)
                    : launch_crt<4, 512, 4, true>(r, out, RL, RLc);
     case 2:
+        if (mp) return one ? launch_crt<2, 512, 9, false, true>(r, out, RL, RLc)
+                           : launch_crt<2, 512, 4, true, true>(r, out, RL, RLc);
         return one ? launch_crt<2, 512, 9, false>(r, out, RL, RLc)
                    : launch_crt<2, 512, 4, true>(r, out, RL, RLc);
     default:
+        if (mp) return one ? launch_crt<1, 512, 9, false, true>(r, out, RL, RLc)
+                           : launch_crt<1, 512, 4, true, true>(r, out, RL, RLc);
         return one ? launch_crt<1, 512, 9, false>(r, out, RL, RLc)
                    : launch_crt<1, 512, 4, true>(r, out, RL, RLc);
     }
@@ -1052,9 +1089,17 @@ int mfh_rns_create(mfh_rns **out, int n, int L)
     r->nmk = (r->nm + 31) / 32 * 32;
     r->KB = kres_blocks(L);
     r->Jpad = (2 * (2 * L + 1) + 63) / 64 * 64;
-    r->crt_eb = 0;
-    for (int eb : {4, 2, 1})
-        if (crt_lds_bytes(eb, 512, r->nmk / 32, r->Jpad) <= 150 * 1024) { r->crt_eb = eb; break; }
+    // the most elements per CRT workgroup whose LDS fits in at most four
+    // passes over the output chunks
+    r->crt_eb = r->crt_nh = 0;
+    for (int eb : {4, 2, 1}) {
+        for (int nh = 1; nh <= 4 && !r->crt_eb; ++nh)
+            if (crt_lds_bytes(eb, 512, r->nmk / 32, r->Jpad, nh) <= 150 * 1024) {
+                r->crt_eb = eb;
+                r->crt_nh = nh;
+            }
+        if (r->crt_eb) break;
+    }
     if (!r->crt_eb) { delete r; return MFH_E_BOUND; }
     r->dev = 0;
     if (hipSetDevice(0) != hipSuccess || hipStreamCreate(&r->stream) != hipSuccess) {

@@ -167,3 +167,19 @@ def test_rns_full_size_equals_mfft(gpu, orc, lib, n, W, signed):
     A = orc.bigmat_rand(n, L, SEED)
     B = orc.bigmat_rand(n, L, SEED_B)
     assert orc.freivalds(A, B, n, L, got, 2 * L + 1, signed_top=signed, nprimes=2)
+
+
+@pytest.mark.parametrize("n,L", [(20, 300), (33, 512), (8, 8)])
+def test_rns_crt_passes_repeat(gpu, orc, n, L):
+    """The CRT of wide outputs runs in passes over output chunks, each
+    carrying into the next (L = 300 and 512: four and three passes); a
+    single-pass kernel must start from a zero carry whatever its LDS held.
+    Two products in a row on one context, the second with a shorter output,
+    both equal to the oracle."""
+    print(f"[rns crt passes] n={n} L={L}", flush=True)
+    A = orc.bigmat_rand(n, L, 71 + L)
+    B = orc.bigmat_rand(n, L, 72 + n)
+    with gpu.Rns(n, L) as r:
+        for RL, signed in ((2 * L + 1, True), (L + 3, False)):
+            want = expected(orc, A, B, n, L, RL, signed)
+            assert np.array_equal(r.mm(A, B, RL, signed=signed), want), (RL, signed)
