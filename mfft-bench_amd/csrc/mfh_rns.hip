@@ -45,6 +45,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "mfh_internal.hpp"
@@ -620,27 +621,36 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
     // that hold output limbs
     auto pass = [&](const int c0, const int c1, const int G0, const int Gb) {
     // 2. byte columns: GEMM over the y digits, q M subtracted, groups of 4.
-    //    A wave takes chunks of 64 output bytes (4 fragment rows); the T
-    //    fragments of a chunk stream in batches of KBB k blocks, the next
+    //    The work is fragment rows of 16 output bytes (a chunk is 4).  Whole
+    //    chunks are dealt to the waves in full rounds; after at least one
+    //    full round the rows of the remaining chunks are split into one run
+    //    of consecutive rows per wave, so that no SIMD gets a chunk more than
+    //    another (2048 bits: 9 chunks over 8 waves, one row each of the
+    //    ninth: CRT 1.22 -> 1.10 ms).  Fewer chunks than waves stay whole
+    //    (512 bits: 3 chunks over 4 waves; split into runs of 3 rows they
+    //    ran 2 % slower, the workgroups sharing a CU already filling it).
+    //    Every T fragment of a row serves all EB element blocks, and every y
+    //    fragment all rows of a run.  The T fragments stream in batches of KBB k blocks, the next
     //    batch loaded while the current one is multiplied (DBL), or arrive
     //    all at once.
-    for (int ch = c0 + wave; ch < c1; ch += NW) {
-        v4i acc[4][EB];
+    auto rows = [&](auto nrc, const int row0) {
+        constexpr int NR = decltype(nrc)::value;
+        v4i acc[NR][EB];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
+        for (int jj = 0; jj < NR; ++jj)
 #pragma unroll
             for (int cb = 0; cb < EB; ++cb) acc[jj][cb] = v4i{0, 0, 0, 0};
-        const v4i *tp = T + (size_t)4 * ch * KBc * 64 + lane;
-        v4i ta[KBB][4], tb[DBL ? KBB : 1][4];
-        auto load = [&](v4i (&t)[KBB][4], int kb0) {
+        const v4i *tp = T + (size_t)row0 * KBc * 64 + lane;
+        v4i ta[KBB][NR], tb[DBL ? KBB : 1][NR];
+        auto load = [&](v4i (&t)[KBB][NR], int kb0) {
 #pragma unroll
             for (int b = 0; b < KBB; ++b)
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
+                for (int jj = 0; jj < NR; ++jj)
                     t[b][jj] = kb0 + b < KBc ? tp[((size_t)jj * KBc + kb0 + b) * 64]
                                              : v4i{0, 0, 0, 0};
         };
-        auto mul = [&](const v4i (&t)[KBB][4], int kb0) {
+        auto mul = [&](const v4i (&t)[KBB][NR], int kb0) {
 #pragma unroll
             for (int b = 0; b < KBB; ++b) {
                 if (kb0 + b >= KBc) continue;
@@ -649,7 +659,7 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
                 for (int cb = 0; cb < EB; ++cb)
                     yf[cb] = yl[((size_t)(kb0 + b) * EB + cb) * 64 + lane];
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
+                for (int jj = 0; jj < NR; ++jj)
 #pragma unroll
                     for (int cb = 0; cb < EB; ++cb)
                         acc[jj][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(t[b][jj], yf[cb],
@@ -668,11 +678,11 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
             mul(ta, 0);
         }
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
+        for (int jj = 0; jj < NR; ++jj)
 #pragma unroll
             for (int cb = 0; cb < EB; ++cb) {
                 const int el = 16 * cb + (lane & 15);
-                const int gi = 4 * (4 * ch + jj) + (lane >> 4);
+                const int gi = 4 * (row0 + jj) + (lane >> 4);
                 const long long q = qv[el];
                 long long g = 0;
 #pragma unroll
@@ -680,6 +690,16 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
                     g = g * 256 + ((long long)acc[jj][cb][v] - q * (long long)mb[4 * gi + v]);
                 grp[(size_t)(gi - G0) * E + el] = g;
             }
+    };
+    const int cfull = c1 - c0 >= NW ? c0 + (c1 - c0) / NW * NW : c1, R = 4 * (c1 - cfull);
+    for (int ch = c0 + wave; ch < cfull; ch += NW) rows(std::integral_constant<int, 4>{}, 4 * ch);
+    if (R > 0) {                        // R < 4 NW: runs of at most 4 rows
+        const int rpw = (R + NW - 1) / NW, r0 = wave * rpw, cnt = min(rpw, R - r0);
+        const int row0 = 4 * cfull + r0;
+        if (cnt == 4) rows(std::integral_constant<int, 4>{}, row0);
+        else if (cnt == 3) rows(std::integral_constant<int, 3>{}, row0);
+        else if (cnt == 2) rows(std::integral_constant<int, 2>{}, row0);
+        else if (cnt == 1) rows(std::integral_constant<int, 1>{}, row0);
     }
     __syncthreads();
 
