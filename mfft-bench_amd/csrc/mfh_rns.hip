@@ -35,7 +35,13 @@
 //      values of weight 2^(32 g), and the groups are carried into RL uint16
 //      limbs by carry lookahead.  Everything is computed modulo
 //      256^Jpad, Jpad >= 2 (2L+1) bytes: the RL <= 2L+1 output limbs are
-//      exact; limbs beyond 2L+1 are the sign extension.
+//      exact; limbs beyond 2L+1 are the sign extension.  When 4L is a
+//      multiple of 64 (L a multiple of 16) that would spend a whole 64-byte
+//      chunk on the top limb's 2 bytes: then Jpad = 4L and limb 2L is
+//      floor(C / 2^(32L)) mod 2^16, from C = M (t - q), t = sum_m y_m/p_m:
+//      round(M 2^(-32L) (t - q) - low 2^(-32L)) with low = C mod 2^(32L)
+//      (its top word suffices); the fp64 error, M 2^(-32L) nm^2 2^-53 with
+//      t's summation, is checked on the host to be below 1/16.
 //
 // MFMA: v_mfma_i32_16x16x64_i8.  Operand fragments: lane l holds row l%16 and
 // 16 k bytes 16 (l/16) .. +15 (A and B use the same k order); results: lane
@@ -561,7 +567,7 @@ TileMap tile_map(int tpr, int wx)
 // the single-pass kernels' registers as they were).
 template <int EB, int NT, int KBB, bool DBL, bool MP>
 __global__ __launch_bounds__(NT) void k_rns_crt(
-    const uint16_t *__restrict__ Y, int n, int np_, int nm, int KBc, int Jpad, int nh,
+    const uint16_t *__restrict__ Y, int n, int np_, int nm, int KBc, int Jpad, int nh, double mtop,
     const v4i *__restrict__ T, const int8_t *__restrict__ mb, const RnsMod *__restrict__ mods,
     uint16_t *__restrict__ out, int RL, int RLc)
 {
@@ -575,6 +581,7 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
     double *qs = (double *)(segin + NT);                          // [NT]
     long long *qv = (long long *)(qs + NT);                       // [E]
     long long *cin = qv + E;                                      // [E]: carry into the pass
+    double *qf = (double *)(cin + E);                             // [E]: t - q
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i = blockIdx.y, j0 = blockIdx.x * E;
@@ -613,6 +620,7 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
         double t = 0;
         for (int r = 0; r < SEGS; ++r) t += qs[r * E + tid];
         qv[tid] = (long long)rint(t);
+        qf[tid] = t - rint(t);
         if (MP) cin[tid] = 0;
     }
     __syncthreads();
@@ -713,7 +721,9 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
     // last run may be shorter and runs past it empty: their carry-outs are
     // not used; the carry into the next pass is the last run's exact one,
     // from its propagation with the true carry-in below.
-    const int Gc = (RLc + 1) / 2;
+    // the groups the GEMM covers (with the fp64 top limb, one fewer than
+    // the output needs)
+    const int Gc = min((RLc + 1) / 2, Jpad / 4);
     int len = (Gb - G0 + SEGS - 1) / SEGS;
     if (len < 2) len = 2;
     const int el = tid % E, sg = tid / E;
@@ -751,7 +761,7 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
     if (j0 + el < n) {
         long long cc = segin[sg * E + el];
         uint16_t *o = out + (size_t)i * n + j0 + el;
-        uint32_t top = 0;
+        uint32_t top = 0, wl = 0;
         for (int g = g0; g < g1; ++g) {
             const long long v = cc + grp[(size_t)(g - G0) * E + el];
             const uint32_t w = (uint32_t)v;
@@ -762,7 +772,15 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
                 o[(size_t)(u + 1) * nn] = (uint16_t)(w >> 16);
                 top = w >> 16;
             }
+            wl = w;
             cc = v >> 32;
+        }
+        // limb 2 Gc from fp64 (when the GEMM stops one limb short): C's
+        // value above the Gc groups is an integer within 1/16 of the estimate
+        if (mtop != 0.0 && 2 * Gc < RLc && g1 == Gc && g0 < g1) {
+            const long long tl = llrint(mtop * qf[el] - (double)wl * 0x1p-32);
+            top = (uint32_t)tl & 0xFFFF;
+            o[(size_t)(2 * Gc) * nn] = (uint16_t)top;
         }
         // limbs above 2L+1: the sign extension of limb RLc-1
         if (g1 == Gc && g0 < g1 && RL > RLc) {
@@ -779,7 +797,7 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
         cin[el] = cc;
     }
     };
-    const int Gc = (RLc + 1) / 2;         // groups that hold the RLc output limbs
+    const int Gc = min((RLc + 1) / 2, Jpad / 4);   // groups that hold output limbs
     if constexpr (MP) {
         for (int c0 = 0; c0 < nch && 16 * c0 < Gc; c0 += cpp) {
             const int c1 = min(c0 + cpp, nch);
@@ -794,7 +812,7 @@ __global__ __launch_bounds__(NT) void k_rns_crt(
 size_t crt_lds_bytes(int EB, int NT, int KBc, int Jpad, int nh)
 {
     const int E = 16 * EB, cpp = (Jpad / 64 + nh - 1) / nh;
-    return (size_t)KBc * EB * 1024 + (size_t)16 * cpp * E * 8 + 5 * NT * 8 + 2 * E * 8;
+    return (size_t)KBc * EB * 1024 + (size_t)16 * cpp * E * 8 + 5 * NT * 8 + 3 * E * 8;
 }
 
 // ---- host planning ---------------------------------------------------------
@@ -870,6 +888,7 @@ int kres_blocks(int L)
 
 struct mfh_rns {
     int n, np, L, nm, nmk, KB, Jpad, crt_eb, crt_nh;
+    double mtop;          // M / 2^(8 Jpad) when limb 2L comes from fp64, else 0
     int cus;              // compute units (8 XCDs of cus / 8)
     int dev;
     hipStream_t stream;
@@ -955,6 +974,13 @@ int rns_tables(mfh_rns *r)
     // CRT: the balanced bytes of M and of each M/p_m
     std::vector<int8_t> mbh(Jpad);
     balanced_bytes(M, Jpad, mbh.data());
+    if (r->mtop != 0.0) {
+        // M / 2^(8 Jpad) from M's top three words (relative error 2^-64)
+        const size_t k = M.size();
+        double v = 0;
+        for (size_t w = k; w-- > 0 && w + 3 >= k;) v = v * 4294967296.0 + (double)M[w];
+        r->mtop = ldexp(v, 32 * (int)(k >= 3 ? k - 3 : 0) - 8 * Jpad);
+    }
     std::vector<int8_t> T((size_t)(Jpad / 16) * KBc * 1024, 0);
     std::vector<int8_t> dm(Jpad);
     std::vector<uint32_t> Mm(M.size());
@@ -1029,7 +1055,8 @@ int launch_crt(const mfh_rns *r, uint16_t *out, int RL, int RLc)
     }
     dim3 grid((r->n + 16 * EB - 1) / (16 * EB), r->n);
     hipLaunchKernelGGL((k_rns_crt<EB, NT, KBB, DBL, MP>), grid, dim3(NT), lds, r->stream, r->dY,
-                       r->n, r->np, r->nm, KBc, r->Jpad, r->crt_nh, (const v4i *)r->dT, r->dMb,
+                       r->n, r->np, r->nm, KBc, r->Jpad, r->crt_nh, r->mtop, (const v4i *)r->dT,
+                       r->dMb,
                        (const RnsMod *)r->dMod, out, RL, RLc);
     MFH_HIP(hipGetLastError());
     return MFH_OK;
@@ -1108,7 +1135,17 @@ int mfh_rns_create(mfh_rns **out, int n, int L)
     r->nm = (int)r->primes.size();
     r->nmk = (r->nm + 31) / 32 * 32;
     r->KB = kres_blocks(L);
-    r->Jpad = (2 * (2 * L + 1) + 63) / 64 * 64;
+    // bytes of the CRT columns: 2 (2L+1), rounded up to 64-byte chunks;
+    // when 4L fills whole chunks, 4L and limb 2L from fp64 (error bound
+    // M 2^(-32L) nm^2 2^-53 below 1/16)
+    {
+        double lgM = 0;
+        for (int p : r->primes) lgM += log2((double)p);
+        const double err = exp2(lgM - 32.0 * L) * (double)r->nm * r->nm * 0x1p-53;
+        const bool top = (4 * L) % 64 == 0 && err < 1.0 / 16;
+        r->Jpad = top ? 4 * L : (2 * (2 * L + 1) + 63) / 64 * 64;
+        r->mtop = top ? 1.0 : 0.0;          // the value is set with the tables
+    }
     // the most elements per CRT workgroup whose LDS fits in at most four
     // passes over the output chunks
     r->crt_eb = r->crt_nh = 0;

@@ -89,3 +89,37 @@ def test_fp64_reduction_needs_no_fixup(lib):
         r = (v - q.astype(np.int64) * p)
         assert np.abs(r).max() <= h, p
         assert np.array_equal(np.mod(r - v, p), np.zeros_like(r))
+
+
+@pytest.mark.parametrize("n,L", [(1024, 128), (4096, 32), (256, 512), (64, 64), (16, 16)])
+def test_fp64_top_limb(lib, n, L):
+    """When 4L fills whole 64-byte chunks the CRT computes C mod 2^(32L) by
+    the GEMM and the top limb as round(M 2^(-32L) (t - q) - w 2^-32), t =
+    sum_m y_m fl(1/p_m) summed in fp64, q = rint(t), w the top 32-bit word
+    of C mod 2^(32L).  Against Python integers: floor(C / 2^(32L)) for
+    random and extreme signed products |C| <= n 2^(2W) (the kernel's error
+    bound, M 2^(-32L) nm^2 2^-53, is far below 1/2 at these plans)."""
+    import math
+    import random
+    from fractions import Fraction
+    import mfft_ctypes
+    ps = [int(p) for p in mfft_ctypes.rns_primes(n, L)]
+    M = math.prod(ps)
+    W = 16 * L
+    mtop = float(Fraction(M, 1 << (32 * L)))
+    cinv = [pow((M // p) % p, -1, p) for p in ps]
+    lim = n * (1 << (2 * W))
+    rnd = random.Random(n + L)
+    cases = [lim, lim - 1, -lim, -lim + 1, 0, -1, 1, 1 << (32 * L), -(1 << (32 * L))]
+    cases += [rnd.randrange(-lim, lim + 1) for _ in range(40)]
+    for C in cases:
+        t = 0.0
+        for p, ci in zip(ps, cinv):
+            r = C * ci % p
+            if r > p // 2:
+                r -= p
+            t += float(r) * (1.0 / p)
+        q = round(t)
+        w = (C % (1 << (32 * L))) >> (32 * L - 32)
+        est = mtop * (t - q) - w * 2.0 ** -32
+        assert abs(est - (C >> (32 * L))) < 1e-3, (C, est)
