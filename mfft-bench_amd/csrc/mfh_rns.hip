@@ -1096,6 +1096,34 @@ void rns_mark(mfh_rns *r, int k)
     if (r->timing) (void)hipEventRecord(r->ev[k], r->stream);
 }
 
+// the product: B transposed, the residues of both operands, the per-prime
+// GEMMs and the CRT into RL limbs at out
+int rns_run(mfh_rns *r, int sgn, const void *dA, const void *dB, uint16_t *out, int RL)
+{
+    rns_mark(r, 0);
+    int rc = mfh_launch_transpose(dB, r->dBt, r->L, r->n, 2, r->stream);
+    if (!rc) rc = run_residue(r, (const uint16_t *)dA, sgn, 0, r->dRA);
+    if (!rc) rc = run_residue(r, r->dBt, sgn, 1, r->dRB);
+    if (rc) return rc;
+    rns_mark(r, 1);
+    const int wx = r->cus / 8;               // persistent workgroups per XCD
+    // eight waves of 32 x 64 (two per SIMD); four waves of 64 x 64 spilled
+    // and ran 1.8x slower
+    const TileMap tm = tile_map(r->np / 128, wx);
+    const int N = r->nm * tm.tpr * tm.tpr, blk = tm.BR * tm.BC;
+    const int R = ((N + 7) / 8 + blk - 1) / blk * blk;
+    hipLaunchKernelGGL(k_rns_pointwise<2>, dim3(8 * wx), dim3(512), 0, r->stream,
+                       (const uint16_t *)r->dRA, (const uint16_t *)r->dRB,
+                       (const RnsMod *)r->dMod, r->nm, r->np, r->dY, wx, tm, R);
+    MFH_HIP(hipGetLastError());
+    rns_mark(r, 2);
+    const int RLc = std::min(RL, 2 * r->L + 1);
+    rc = run_crt(r, out, RL, RLc);
+    if (rc) return rc;
+    rns_mark(r, 3);
+    return MFH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1209,29 +1237,7 @@ int mfh_rns_mm_dev(mfh_rns *r, int in_kind, const void *dA, const void *dB, void
 {
     if (!r || !dA || !dB || !dOut || RL < 1) return MFH_E_ARG;
     if (in_kind != MFH_IN_U16 && in_kind != MFH_IN_U16_SIGNED) return MFH_E_ARG;
-    const int sgn = in_kind == MFH_IN_U16_SIGNED;
-    rns_mark(r, 0);
-    int rc = mfh_launch_transpose(dB, r->dBt, r->L, r->n, 2, r->stream);
-    if (!rc) rc = run_residue(r, (const uint16_t *)dA, sgn, 0, r->dRA);
-    if (!rc) rc = run_residue(r, r->dBt, sgn, 1, r->dRB);
-    if (rc) return rc;
-    rns_mark(r, 1);
-    const int wx = r->cus / 8;               // persistent workgroups per XCD
-    // eight waves of 32 x 64 (two per SIMD); four waves of 64 x 64 spilled
-    // and ran 1.8x slower
-    const TileMap tm = tile_map(r->np / 128, wx);
-    const int N = r->nm * tm.tpr * tm.tpr, blk = tm.BR * tm.BC;
-    const int R = ((N + 7) / 8 + blk - 1) / blk * blk;
-    hipLaunchKernelGGL(k_rns_pointwise<2>, dim3(8 * wx), dim3(512), 0, r->stream,
-                       (const uint16_t *)r->dRA, (const uint16_t *)r->dRB,
-                       (const RnsMod *)r->dMod, r->nm, r->np, r->dY, wx, tm, R);
-    MFH_HIP(hipGetLastError());
-    rns_mark(r, 2);
-    const int RLc = std::min(RL, 2 * r->L + 1);
-    rc = run_crt(r, (uint16_t *)dOut, RL, RLc);
-    if (rc) return rc;
-    rns_mark(r, 3);
-    return MFH_OK;
+    return rns_run(r, in_kind == MFH_IN_U16_SIGNED, dA, dB, (uint16_t *)dOut, RL);
 }
 
 int mfh_rns_mm(mfh_rns *r, int in_kind, const uint16_t *A, const uint16_t *B, uint16_t *out,
@@ -1270,6 +1276,8 @@ int rns_fpx(mfh_rns *r, int f64, const void *dA, const void *dB, int SA, int SB,
     if (r->L < 2) return MFH_E_ARG;
     const int Lg = r->L - 1, RLr = 2 * r->L;
     const size_t nn = (size_t)r->n * r->n;
+    // (a decode inside the CRT kernel, one thread per element from the
+    // carried words in LDS, ran 2 % slower than this separate pass)
     int rc = MFH_OK;
     if (!r->dFO) {
         rc = rns_alloc(r, (void **)&r->dFA, (size_t)r->L * nn * 2);
@@ -1279,7 +1287,7 @@ int rns_fpx(mfh_rns *r, int f64, const void *dA, const void *dB, int SA, int SB,
     }
     if ((rc = mfh_launch_encode_tc(dA, f64, r->n, Lg, SA, r->dFA, r->stream))) return rc;
     if ((rc = mfh_launch_encode_tc(dB, f64, r->n, Lg, SB, r->dFB, r->stream))) return rc;
-    if ((rc = mfh_rns_mm_dev(r, MFH_IN_U16_SIGNED, r->dFA, r->dFB, r->dFO, RLr))) return rc;
+    if ((rc = rns_run(r, 1, r->dFA, r->dFB, r->dFO, RLr))) return rc;
     return mfh_launch_decode_limbs(r->dFO, nn, RLr, SA + SB, f64 ? MFH_DEC_F64 : MFH_DEC_F32,
                                    dC, nullptr, r->stream);
 }

@@ -14,6 +14,7 @@
 #include <utility>
 
 #include "mfh_internal.hpp"
+#include "mfh_decode.hpp"
 
 namespace {
 
@@ -843,109 +844,6 @@ __device__ __forceinline__ long long bperm64(long long v, int addr)
     return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
 }
 
-// ---- fixed-point decode (src/fpfixed.c:212-322) ------------------------------
-// Carry over RL = 2L+2 limbs with an arithmetic shift, take the magnitude
-// (two's complement negation when the final carry is negative), keep the
-// top <= 4 limbs below the highest non-zero one plus a sticky bit, round to
-// 24 bits half-even, and scale by 2^-(SA+SB).  Exact zero gives +0.0f.
-// Streaming: both the value and its negation are tracked limb by limb, so no
-// per-element limb array is needed.
-struct TopTrack {
-    int h;
-    uint32_t hist[4];      // limbs w-3 .. w
-    uint32_t win[4];       // limbs h-3 .. h when h was set
-    uint32_t below;        // OR of limbs < w-3
-    uint32_t sticky;       // OR of limbs < h-3 when h was set
-    __device__ void init()
-    {
-        h = -1; below = 0; sticky = 0;
-        for (int q = 0; q < 4; ++q) { hist[q] = 0; win[q] = 0; }
-    }
-    __device__ void push(int w, uint32_t limb)
-    {
-        below |= hist[0];
-        hist[0] = hist[1]; hist[1] = hist[2]; hist[2] = hist[3]; hist[3] = limb;
-        if (limb) {
-            h = w;
-            for (int q = 0; q < 4; ++q) win[q] = hist[q];
-            sticky = below;
-        }
-    }
-};
-
-// FMT: MFH_DEC_F32 rounds to 24 bits and writes fp32, MFH_DEC_F64 to 53
-// bits and fp64 (src/fpfixed.c:308-322), MFH_DEC_SIG63 to 63 bits and writes
-// the signed significand and the exponent of the long double decode
-// (src/fpfixed.c:292-306: int64 sig at out, int32 exponent at out2).
-// Decode of one element from its 2L-1 coefficient planes (plane(w), w < P)
-// over RL limbs (src/fpfixed.c:212-322, see k_decode)
-template <int FMT, class Plane>
-__device__ __forceinline__ void decode_value(const Plane &plane, int P, int RL, int SAB,
-                                             void *__restrict__ out_, int32_t *__restrict__ out2,
-                                             size_t e)
-{
-    constexpr int BITS = FMT == MFH_DEC_F32 ? 24 : FMT == MFH_DEC_F64 ? 53 : 63;
-    TopTrack pos, neg;
-    pos.init(); neg.init();
-    int64_t carry = 0;
-    uint32_t borrow = 1;
-    for (int w = 0; w < RL; ++w) {
-        int64_t t = carry + (w < P ? plane(w) : 0);
-        uint32_t limb = (uint32_t)(t & 0xFFFF);
-        carry = t >> 16;
-        uint32_t nl = ((~limb) & 0xFFFFu) + borrow;
-        borrow = nl >> 16;
-        nl &= 0xFFFFu;
-        pos.push(w, limb);
-        neg.push(w, nl);
-    }
-    const bool isneg = carry < 0;
-    const int h = isneg ? neg.h : pos.h;
-    if (h < 0) {
-        if constexpr (FMT == MFH_DEC_F32) ((float *)out_)[e] = 0.0f;
-        else if constexpr (FMT == MFH_DEC_F64) ((double *)out_)[e] = 0.0;
-        else { ((long long *)out_)[e] = 0; out2[e] = 0; }
-        return;
-    }
-    uint32_t win[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) win[q] = isneg ? neg.win[q] : pos.win[q];
-    const uint32_t sticky = isneg ? neg.sticky : pos.sticky;
-    int bl = 32 - __clz(win[3]);
-    const int k = h + 1 < 4 ? h + 1 : 4;
-    unsigned long long top = 0;
-#pragma unroll
-    for (int q = 3; q >= 0; --q)
-        if (q > 3 - k) top = (top << 16) | win[q];
-    // limbs below the gathered ones: win[0 .. 3-k] (positions h-3 .. h-k)
-    // only exist when k == 4, so sticky is the OR below h-3.
-    const int base = 16 * (h - k + 1);
-    int tb = 16 * h + bl - base;
-    int shift = base;
-    unsigned long long sig = top;
-    // a window of at most BITS bits is returned as it stands (sticky unused)
-    if (tb > BITS) {
-        int drop = tb - BITS;
-        sig = top >> drop;
-        unsigned long long rem = top & ((1ULL << drop) - 1);
-        unsigned long long half = 1ULL << (drop - 1);
-        int up = rem > half ? 1 : rem < half ? 0 : (sticky ? 1 : (int)(sig & 1));
-        sig += (unsigned long long)up;
-        if (sig >> BITS) { sig >>= 1; drop++; }
-        shift += drop;
-    }
-    if constexpr (FMT == MFH_DEC_F32) {
-        float v = ldexpf((float)sig, shift - SAB);
-        ((float *)out_)[e] = isneg ? -v : v;
-    } else if constexpr (FMT == MFH_DEC_F64) {
-        double v = ldexp((double)sig, shift - SAB);
-        ((double *)out_)[e] = isneg ? -v : v;
-    } else {
-        ((long long *)out_)[e] = isneg ? -(long long)sig : (long long)sig;
-        out2[e] = shift - SAB;
-    }
-}
-
 //
 // CARRY: instead of writing Cw, one thread per element (all in the first
 // wave, E <= 64) propagates the carries through the element's 2L-1 planes
@@ -1240,10 +1138,9 @@ __global__ __launch_bounds__(256) void k_encode_tc(Src src, uint16_t *__restrict
     }
 }
 
-// The fixed-point decode (decode_value) from RLr carried two's complement
-// limbs: limb w as a plane, the top one sign-extended.  The decode carries
-// them again (a no-op) over one more limb, so the window and the rounding
-// are those of the coefficient-plane decode of the same value.
+// The fixed-point decode from RLr carried two's complement limbs
+// (decode_carried: the same sign, window and rounding as the
+// coefficient-plane decode of the same value, found from the top limb down)
 template <int FMT>
 __global__ __launch_bounds__(256) void k_decode_limbs(const uint16_t *__restrict__ limbs,
                                                       size_t nn, int RLr, int SAB,
@@ -1251,12 +1148,8 @@ __global__ __launch_bounds__(256) void k_decode_limbs(const uint16_t *__restrict
 {
     const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= nn) return;
-    decode_value<FMT>(
-        [&](int w) -> int64_t {
-            const uint16_t x = limbs[(size_t)w * nn + e];
-            return w == RLr - 1 ? (int64_t)(int16_t)x : (int64_t)x;
-        },
-        RLr, RLr + 1, SAB, out, out2, e);
+    decode_carried<FMT>([&](int w) -> uint32_t { return limbs[(size_t)w * nn + e]; }, RLr, SAB,
+                        out, out2, e);
 }
 
 // ---- plane transpose (B operand) -----------------------------------------------
