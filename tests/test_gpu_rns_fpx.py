@@ -163,3 +163,28 @@ def test_rns_fpx_full_size_equals_mfft(gpu, lib, n, W, f64):
     bad = np.nonzero(got != want)[0]
     assert bad.size == 0, f"{bad.size} outputs differ, first at {bad[:5]}"
     assert np.count_nonzero(want) > n * n // 2
+
+
+def test_rns_fpx_limb_boundaries(gpu, orc):
+    """Diagonal products +-2^k and +-(2 - 2^-23) 2^k for 64 consecutive
+    exponents k (so every position modulo a 16-bit limb, whatever the
+    grid's scale): the decode of carried limbs meets negative values whose
+    magnitude is exactly a power of 2^16 (every limb below its window zero)
+    and all-ones significands; the off-diagonal outputs are +0.0f."""
+    n = 64
+    A = np.zeros(n * n, np.float32)
+    B = np.zeros(n * n, np.float32)
+    for i in range(n):
+        k, ea = -40 + i, i % 7 - 3
+        ma = 1.0 if i % 4 else 2.0 - 2.0 ** -23
+        A[i * n + i] = np.float32(np.ldexp(ma, ea) * (-1 if i % 2 else 1))
+        B[i * n + i] = np.float32(np.ldexp(1.0, k - ea) * (-1 if i % 5 == 0 else 1))
+    want, L, SA, SB = oracle_f32(orc, A, B, n, 512)
+    with gpu.Rns(n, L + 1) as r:
+        got = r.fpx_mm(A, B, SA, SB)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    d = np.arange(n) * (n + 1)
+    assert np.count_nonzero(want[d]) == n
+    off = np.ones(n * n, bool)
+    off[d] = False
+    assert np.all(got[off].view(np.uint32) == 0)
