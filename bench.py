@@ -248,6 +248,7 @@ def rns_measure(n, L, kind, dA, dB, steps, warmup, want=None, fpx_scale=None):
                          "crt_carry": round(st[2], 3)},
             "int8_ops": {"residues": res_ops, "per_prime_gemms": pw_ops, "crt": crt_ops},
             "per_prime_gemm_tops": round(pw_ops / (st[1] * 1e-3) / 1e12, 1),
+            "per_prime_gemm_frac": round(pw_ops / (st[1] * 1e-3) / 5.0e15, 4),
             "device_bytes": nbytes, "equal_to_mfft": equal,
             "note": (("fp32 product on the same grid by residues mod 16-bit primes "
                       "(mfh_rns_fpx_mm_dev: encode to L+1 two's complement limbs, exact "
