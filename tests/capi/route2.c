@@ -190,6 +190,25 @@ int r2_fpx_f32(const float *A, const float *B, int n, int force_bits, float *C_c
     return rc;
 }
 
+/* The fixed-point product by the multi-modular path from C: the grid of
+ * fpx_init (L, SA, SB) on a context of L + 1 limbs, mfh_rns_fpx_mm on the
+ * caller's host arrays.  Returns 0, a negative library code, or -101 for an
+ * init failure. */
+int r2_rns_fpx_f32(const float *A, const float *B, int n, int force_bits, float *C_out)
+{
+    fpx_ctx f;
+    if (fpx_init(&f, A, B, n, force_bits) != 0) return -101;
+    const int L = f.L, SA = f.SA, SB = f.SB;
+    fpx_free(&f);
+    mfh_rns *r = NULL;
+    int rc = mfh_rns_create(&r, n, L + 1);
+    if (!rc) {
+        rc = mfh_rns_fpx_mm(r, A, B, SA, SB, C_out);
+        mfh_rns_destroy(r);
+    }
+    return rc;
+}
+
 /* src/mlgemm.c:731-736 on the device: fpx_init_d, fpx_encode_d, conv_mfft,
  * fpx_decode_f64 and fpx_decode_ld, then the fused fpx_mm_f64 after the
  * inputs are gone. */

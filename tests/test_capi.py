@@ -45,6 +45,7 @@ def r2(lib):
     d.r2_fpx_f32.argtypes = [vp, vp, i, i, vp, vp, vp]
     d.r2_fpx_f64.argtypes = [vp, vp, i, i, vp, vp, vp, vp]
     d.r2_rns_mm.argtypes = [i, i, u64, u64, i, vp, i, vp]
+    d.r2_rns_fpx_f32.argtypes = [vp, vp, i, i, vp]
     return d
 
 
@@ -190,6 +191,23 @@ def test_route2_fpx_f32_fixture(gpu, r2, case):
     assert L.value == 32
     assert np.array_equal(conv.view(np.uint32), want)
     assert np.array_equal(fused.view(np.uint32), want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", range(3))
+def test_route2_rns_fpx_f32_fixture(gpu, r2, case):
+    """the multi-modular fixed-point product called from C (fpx_init for the
+    grid, mfh_rns_create with one limb more, mfh_rns_fpx_mm) against the
+    Fraction fixtures"""
+    with open(os.path.join(GOLD, "fpx.json")) as f:
+        c = json.load(f)[case]
+    n = c["n"]
+    A = np.array(c["A_bits"], dtype=np.uint32).view(np.float32)
+    B = np.array(c["B_bits"], dtype=np.uint32).view(np.float32)
+    want = np.array(c["C_bits"], dtype=np.uint32)
+    out = np.full(n * n, np.nan, np.float32)
+    assert r2.r2_rns_fpx_f32(A.ctypes.data, B.ctypes.data, n, 512, out.ctypes.data) == 0
+    assert np.array_equal(out.view(np.uint32), want)
 
 
 @pytest.mark.gpu
