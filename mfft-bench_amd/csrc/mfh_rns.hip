@@ -549,13 +549,14 @@ TileMap tile_map(int tpr, int wx)
 
 // ---- 3. CRT and carry ------------------------------------------------------
 // E = 16 EB elements (row i = blockIdx.y, columns j0 .. j0+E-1) per
-// workgroup of 8 waves.  LDS: the y digit pairs of the E elements as MFMA B
-// fragments [KBc][EB][64 lanes][16 B] (fragment (kb, cb): element
-// 16 cb + l%16, the digit pairs of primes 32 kb + 8 (l/16) .. +7), the
-// int64 groups [G = Jpad/4][E], the carry lookahead's run data, and q's
-// partial fp64 sums and values.  T holds the A fragments [Jpad/16][KBc][64][16 B]: row j (output
-// byte) of k = 2m + d is byte j of M/p_m (d = 0) or of 256 M/p_m (d = 1),
-// zero for m >= nm.
+// workgroup of NT / 64 waves.  LDS: the y digit pairs of the E elements as
+// MFMA B fragments [KBc][EB][64 lanes][16 B] (fragment (kb, cb): element
+// 16 cb + l%16, the digit pairs of primes 32 kb + 8 (l/16) .. +7), one
+// pass's int64 groups [16 cpp][E], the carry lookahead's run data, q's
+// partial fp64 sums, q, t - q and the carry into the pass per element.  T
+// holds the A fragments [Jpad/16][KBc][64][16 B]: row j (output byte) of
+// k = 2m + d is byte j of M/p_m (d = 0) or of 256 M/p_m (d = 1), zero for
+// m >= nm.
 // NT threads (512, or 256 for narrow outputs of at most four chunks);
 // KBB: the T fragments of a chunk are loaded in batches of KBB k blocks,
 // double-buffered (DBL), or all at once (KBB >= KBc, one wait per chunk).
