@@ -274,7 +274,7 @@ int  mfh_rns_residues_dev(mfh_rns *ctx, int in_kind, const void *dX, void *dR);
  * of the two's complement operands).  Same inputs, scales and single
  * rounding as mfh_fpx_mm_dev on an L-limb context, so the same outputs bit
  * for bit.  The first call allocates the encoded operands and product
- * limbs ((4 L + 4) n^2 bytes, kept with the context). */
+ * limbs ((8 L + 8) n^2 bytes, kept with the context). */
 int  mfh_rns_fpx_mm_dev(mfh_rns *ctx, const void *dA, const void *dB, int SA, int SB,
                         void *dC);
 int  mfh_rns_fpx_mm_f64_dev(mfh_rns *ctx, const void *dA, const void *dB, int SA, int SB,
