@@ -45,3 +45,54 @@ def test_sweep_n_rows_exact(gpu, n):
     rows = _rows(n, 256, signed=(n == 96))
     for r in rows:
         assert r[-1] == "yes", r
+
+
+def _bench_json(argv):
+    import json
+    import bench
+    buf = io.StringIO()
+    old = sys.argv
+    sys.argv = ["bench.py"] + argv
+    try:
+        with contextlib.redirect_stdout(buf):
+            bench.main()
+    finally:
+        sys.argv = old
+    return json.loads([line for line in buf.getvalue().splitlines() if line.startswith("{")][-1])
+
+
+def test_bench_line_multimodular_equal(gpu):
+    """bench.py's JSON line at the 1024-bit workload: the MFFT product and,
+    beside it, the multi-modular product of the same device inputs with
+    limbs equal to the MFFT's; --rns-only runs the latter alone"""
+    d = _bench_json(["--config", "c1", "--steps", "2", "--warmup", "1", "--no-cpu-baseline"])
+    assert d["value"] > 0 and d["n_gpus"] == 1
+    mm = d["multimodular"]
+    assert mm["equal_to_mfft"] is True and mm["primes"] == 129 and mm["ms_per_step"] > 0
+    r = _bench_json(["--rns-only", "--config", "c1", "--steps", "2", "--warmup", "1"])
+    assert r["multimodular"]["primes"] == 129 and r["multimodular"]["ms_per_step"] > 0
+
+
+def test_bench_line_multimodular_fp32_equal(gpu, lib):
+    """bench.py's multi-modular measurement on fp32 inputs (n = 256 on the
+    512-bit grid, entries +-m 2^e, e in [-20, 20]): output bits equal to
+    the MFFT path's on the same device inputs"""
+    import numpy as np
+    import bench
+    n, L, S = 256, 32, 256
+    dA, dB, dC = gpu.DevBuf(n * n * 4), gpu.DevBuf(n * n * 4), gpu.DevBuf(n * n * 4)
+    try:
+        gpu.check(lib.mfh_rand_f32_dev(None, dA.ptr, n * n, 12345, -20, 20))
+        gpu.check(lib.mfh_rand_f32_dev(None, dB.ptr, n * n, 12345 ^ 0xABCDEF, -20, 20))
+        gpu.check(lib.mfh_sync(None))
+        with gpu.Ctx(n, L) as ctx:
+            gpu.check(lib.mfh_fpx_mm_dev(ctx.h, dA.ptr, dB.ptr, S, S, dC.ptr))
+            ctx.sync()
+        want = dC.download(np.uint32, n * n)
+        with contextlib.redirect_stderr(io.StringIO()):
+            mm = bench.rns_measure(n, L, gpu.MFH_IN_U16, dA, dB, 2, 1, want, fpx_scale=(S, S))
+    finally:
+        for b in (dA, dB, dC):
+            b.free()
+    assert np.count_nonzero(want) > n * n // 2
+    assert mm["equal_to_mfft"] is True and mm["primes"] == 67
