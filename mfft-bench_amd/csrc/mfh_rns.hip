@@ -84,6 +84,15 @@ __device__ __forceinline__ int rns_reduce(double v, int p, double invp)
     return (int)fma(-q, (double)p, v);
 }
 
+// The same for an int32 v, with p given as a double: q as above,
+// r = v - q p by one fma (exact: the result is small)
+__device__ __forceinline__ int rns_reduce_i32(int v, double p, double invp)
+{
+    const double vd = (double)v;
+    const double q = rint(vd * invp);
+    return (int)fma(-q, p, vd);
+}
+
 // digit pair of a balanced residue r, |r| <= 32639: with t = r + 128,
 // lo = (t & 255) - 128 and hi = t >> 8, so the pair lo | hi << 8 (as bytes)
 // is t ^ 0x80 in the low 16 bits
@@ -263,16 +272,23 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
         for (int mm = 0; mm < 2; ++mm) {
             const int m = 8 * ob + 2 * grp + mm;
             const RnsMod md = mods[m < nm ? m : 0];
+            const int off0 = scaled ? md.k0b : md.k0, off1 = scaled ? md.k1b : md.k1;
+            const double pd = (double)md.p;
 #pragma unroll
             for (int cb = 0; cb < EB; ++cb) {
-                uint16_t w = 0;
-                if (ok[cb] && m < nm) {
-                    const int off = scaled ? (sb[cb] ? md.k1b : md.k0b) : (sb[cb] ? md.k1 : md.k0);
+                const int off = sb[cb] ? off1 : off0;
+                int rr;
+                if constexpr (KB <= 4) {
+                    // |acc| <= 64 KB 2^14 <= 2^22: 256 acc_hi + acc_lo + off
+                    // is below 2^31 in magnitude, exact in int32
+                    rr = rns_reduce_i32(acc[cb][2 * mm + 1] * 256 + acc[cb][2 * mm] + off, pd,
+                                        md.invp);
+                } else {
                     const double v = (double)acc[cb][2 * mm + 1] * 256.0 +
                                      (double)acc[cb][2 * mm] + (double)off;
-                    w = rns_pair(rns_reduce(v, md.p, md.invp));
+                    rr = rns_reduce(v, md.p, md.invp);
                 }
-                tr[wave][2 * grp + mm][16 * cb + col] = w;
+                tr[wave][2 * grp + mm][16 * cb + col] = ok[cb] && m < nm ? rns_pair(rr) : 0;
             }
         }
         // the wave's 16 EB consecutive elements of 8 primes, 16 bytes per
