@@ -238,19 +238,41 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
     v4i wn[PF > 0 ? PF : 1];
 #pragma unroll
     for (int kb = 0; kb < PF; ++kb) wn[kb] = W[(size_t)kb * 64 + lane];
+    // Up to 2 k blocks (registers to spare) the constants of the lane's two
+    // primes of block ob + 1 also load during block ob
+    constexpr bool MPF = KB <= 2;
+    RnsMod mdn[MPF ? 2 : 1];
+    if constexpr (MPF) {
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+            const int m = 2 * grp + mm;
+            mdn[mm] = mods[m < nm ? m : 0];
+        }
+    }
 #pragma unroll 1
     for (int ob = 0; ob < nob; ++ob) {
         v4i acc[EB];
 #pragma unroll
         for (int cb = 0; cb < EB; ++cb) acc[cb] = v4i{0, 0, 0, 0};
+        // the prefetches are unconditional (the last block loads itself
+        // again): a branch around them had made the compiler wait for every
+        // load where the paths join
+        const int obn = ob + 1 < nob ? ob + 1 : ob;
+        RnsMod mdc[MPF ? 2 : 1];
+        if constexpr (MPF) {
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm) {
+                mdc[mm] = mdn[mm];
+                const int m = 8 * obn + 2 * grp + mm;
+                mdn[mm] = mods[m < nm ? m : 0];
+            }
+        }
         v4i wc[PF > 0 ? PF : 1];
         if constexpr (PF) {
 #pragma unroll
-            for (int kb = 0; kb < PF; ++kb) wc[kb] = wn[kb];
-            if (ob + 1 < nob) {
-#pragma unroll
-                for (int kb = 0; kb < PF; ++kb)
-                    wn[kb] = W[((size_t)(ob + 1) * KB + kb) * 64 + lane];
+            for (int kb = 0; kb < PF; ++kb) {
+                wc[kb] = wn[kb];
+                wn[kb] = W[((size_t)obn * KB + kb) * 64 + lane];
             }
         } else {
             // this wave's copies of block ob (and its earlier stores) are
@@ -271,7 +293,7 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm) {
             const int m = 8 * ob + 2 * grp + mm;
-            const RnsMod md = mods[m < nm ? m : 0];
+            const RnsMod md = MPF ? mdc[MPF ? mm : 0] : mods[m < nm ? m : 0];
             const int off0 = scaled ? md.k0b : md.k0, off1 = scaled ? md.k1b : md.k1;
             const double pd = (double)md.p;
 #pragma unroll
