@@ -211,81 +211,102 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
             if (sgn && kb == (L - 1) / 32) sb[cb] = ok[cb] ? buf[(L - 1) % 32][e] >> 15 : 0;
         }
     }
-    // Weight fragments of output block ob + 1 are in flight while block ob
-    // is multiplied.  Up to 8 k blocks each wave prefetches them into
-    // registers.  Beyond that (the registers hold the element fragments)
-    // the workgroup copies each block once into LDS by buffer-to-LDS copies,
-    // double-buffered, and its four waves read it there (when every wave
-    // loaded the block itself, the weight stream from L2 bounded the kernel
-    // at 16 k blocks: 0.79 ms per operand at 8192 bits, n = 256).
+    // Weight fragments of later blocks of 8 primes are in flight while
+    // block ob is multiplied.  Up to 8 k blocks each wave prefetches block
+    // ob + 1 into registers.  Beyond that (the registers hold the element
+    // fragments) the workgroup copies each block once into LDS by
+    // buffer-to-LDS copies, two blocks ahead into three buffers, and its
+    // four waves read it there (when every wave loaded the block itself, the
+    // weight stream from L2 bounded the kernel at 16 k blocks: 0.79 ms per
+    // operand at 8192 bits, n = 256).  Each buffer is its own array, picked
+    // at compile time (the loop runs in threes): with one array indexed by
+    // the block the compiler waited for the copies just issued into the
+    // next buffer before reading the current one.
     constexpr int PF = KB <= 8 ? KB : 0;
     constexpr int KL = PF ? 1 : KB;
-    __shared__ __align__(16) v4i wl[PF ? 1 : 2][KL][64];
+    __shared__ __align__(16) v4i wl0[KL][64], wl1[PF ? 1 : KL][64], wl2[PF ? 1 : KL][64];
     const int nob = (nm + 7) / 8;            // blocks of 8 primes, the last partial
-    auto wcopy = [&](int ob, int buf) {
+    // copies of block ob (KL / 4 per wave) into buffer B
+    auto wcopy = [&](auto btag, int ob) {
+        constexpr int B = decltype(btag)::value;
+        v4i (*dst)[64] = B == 0 ? wl0 : B == 1 ? wl1 : wl2;
 #pragma unroll
         for (int i = 0; i < KL / 4; ++i) {
             const int kb = wave + 4 * i;
             __builtin_amdgcn_global_load_lds((const void *)(W + ((size_t)ob * KB + kb) * 64 + lane),
-                                             (void *)&wl[buf][kb][0], 16, 0, 0);
+                                             (void *)&dst[kb][0], 16, 0, 0);
+        }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using B2 = std::integral_constant<int, 2>;
+    v4i wn[PF > 0 ? PF : 1];
+    // the constants of the lane's two primes of the next block load during
+    // the current one (up to 2 k blocks, where registers are to spare, and
+    // on the LDS path)
+    constexpr bool MPF = KB <= 2 || !PF;
+    RnsMod mdn[MPF ? 2 : 1];
+    auto mload = [&](int ob) {
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+            const int m = 8 * ob + 2 * grp + mm;
+            mdn[mm] = mods[m < nm ? m : 0];
         }
     };
     if constexpr (PF) {
         if (k0 >= np_) return;                   // past the padded row (after the barriers)
+#pragma unroll
+        for (int kb = 0; kb < PF; ++kb) wn[kb] = W[(size_t)kb * 64 + lane];
+        if constexpr (MPF) mload(0);
     } else {
-        wcopy(0, 0);
+        mload(0);
+        wcopy(B0{}, 0);
+        wcopy(B1{}, nob > 1 ? 1 : 0);
     }
-    v4i wn[PF > 0 ? PF : 1];
-#pragma unroll
-    for (int kb = 0; kb < PF; ++kb) wn[kb] = W[(size_t)kb * 64 + lane];
-    // Up to 2 k blocks (registers to spare) the constants of the lane's two
-    // primes of block ob + 1 also load during block ob
-    constexpr bool MPF = KB <= 2;
-    RnsMod mdn[MPF ? 2 : 1];
-    if constexpr (MPF) {
-#pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
-            const int m = 2 * grp + mm;
-            mdn[mm] = mods[m < nm ? m : 0];
-        }
-    }
-#pragma unroll 1
-    for (int ob = 0; ob < nob; ++ob) {
+    // Block ob, its weights in buffer B (LDS path).  The prefetches are
+    // unconditional (past the end the last block loads itself again): a
+    // branch around them had made the compiler wait for every load where
+    // the paths join.
+    auto block = [&](auto btag, int ob) {
+        constexpr int B = decltype(btag)::value;
         v4i acc[EB];
 #pragma unroll
         for (int cb = 0; cb < EB; ++cb) acc[cb] = v4i{0, 0, 0, 0};
-        // the prefetches are unconditional (the last block loads itself
-        // again): a branch around them had made the compiler wait for every
-        // load where the paths join
         const int obn = ob + 1 < nob ? ob + 1 : ob;
         RnsMod mdc[MPF ? 2 : 1];
-        if constexpr (MPF) {
-#pragma unroll
-            for (int mm = 0; mm < 2; ++mm) {
-                mdc[mm] = mdn[mm];
-                const int m = 8 * obn + 2 * grp + mm;
-                mdn[mm] = mods[m < nm ? m : 0];
-            }
-        }
         v4i wc[PF > 0 ? PF : 1];
         if constexpr (PF) {
+            if constexpr (MPF) {
+#pragma unroll
+                for (int mm = 0; mm < 2; ++mm) mdc[mm] = mdn[mm];
+                mload(obn);
+            }
 #pragma unroll
             for (int kb = 0; kb < PF; ++kb) {
                 wc[kb] = wn[kb];
                 wn[kb] = W[((size_t)obn * KB + kb) * 64 + lane];
             }
         } else {
-            // this wave's copies of block ob (and its earlier stores) are
-            // done; after the barrier every wave's are, and every wave has
-            // finished reading the other buffer (block ob - 1), which the
-            // copies of block ob + 1 then overwrite
-            wait_vm_lgkm<0>();
-            __syncthreads();
-            if (ob + 1 < nob) wcopy(ob + 1, (ob + 1) & 1);
+            // Issue order per block: the constants of block ob + 1, then the
+            // copies of block ob + 2.  Loads complete in order, so with only
+            // the KL / 4 youngest loads (the copies of block ob + 1) left in
+            // flight this wave's copies of block ob and the constants of
+            // block ob have landed; after the barrier every wave's copies
+            // have, and every wave has finished reading buffer (B + 2) % 3
+            // (block ob - 1), which the copies of block ob + 2 then overwrite.
+            // (A plain s_barrier: __syncthreads' fence would wait for every
+            // copy in flight.)
+            wait_vm_lgkm<KL / 4>();
+            __builtin_amdgcn_s_barrier();
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm) mdc[mm] = mdn[mm];
+            mload(obn);
+            wcopy(std::integral_constant<int, (B + 2) % 3>{}, ob + 2 < nob ? ob + 2 : nob - 1);
         }
+        v4i (*wb)[64] = B == 0 ? wl0 : B == 1 ? wl1 : wl2;
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-            const v4i w = PF ? wc[kb < PF ? kb : 0] : wl[PF ? 0 : ob & 1][PF ? 0 : kb][lane];
+            const v4i w = PF ? wc[kb < PF ? kb : 0] : wb[PF ? 0 : kb][lane];
 #pragma unroll
             for (int cb = 0; cb < EB; ++cb)
                 acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w, ef[kb][cb], acc[cb], 0, 0, 0);
@@ -323,6 +344,23 @@ __global__ __launch_bounds__(256) void k_rns_residue(const uint16_t *__restrict_
             const uint4 v = *(const uint4 *)&tr[wave][pm][8 * ch];
             if (m < nm) *(uint4 *)(R + (size_t)m * npp + (size_t)r * np_ + k0 + 8 * ch) = v;
         }
+    };
+    if constexpr (PF) {
+#pragma unroll 1
+        for (int ob = 0; ob < nob; ++ob) block(B0{}, ob);
+    } else {
+        int ob = 0;
+#pragma unroll 1
+        for (; ob + 3 <= nob; ob += 3) {
+            block(B0{}, ob);
+            block(B1{}, ob + 1);
+            block(B2{}, ob + 2);
+        }
+        if (ob < nob) block(B0{}, ob);
+        if (ob + 1 < nob) block(B1{}, ob + 1);
+        // the copies still in flight land before the workgroup's LDS is
+        // given to another
+        wait_vm_lgkm<0>();
     }
 }
 
