@@ -29,10 +29,13 @@ def expected(orc, A, B, n, L, RL, signed):
     return orc.normalize(orc.conv_limbplane(A32, B32, n, L), 2 * L - 1, n, RL)
 
 
-# every residue-kernel instantiation (k blocks 1 .. 16), ragged n, odd L
+# every residue-kernel instantiation (k blocks 1 .. 16), ragged n, odd L;
+# at 16 k blocks the blocks of 8 primes run in threes (three LDS weight
+# buffers): 129, 65 and 130 blocks at L = 511, 257 and 512 end on each
+# buffer
 SIZES = [(1, 1), (1, 2), (5, 4), (8, 8), (16, 16), (13, 32), (8, 64), (7, 128), (3, 256),
          (6, 512), (64, 64), (70, 32), (100, 16), (130, 8), (129, 33), (257, 3), (2, 512),
-         (40, 100), (24, 200), (9, 300)]
+         (40, 100), (24, 200), (9, 300), (12, 511), (8, 257)]
 
 
 @pytest.mark.parametrize("signed", [False, True])
